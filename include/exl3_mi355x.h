@@ -1,0 +1,131 @@
+/* SPDX-License-Identifier: Apache-2.0
+ *
+ * exl3_mi355x: C ABI of the MI355X (gfx950) EXL3 quantized-linear hot path.
+ *
+ * Every kernel the reference (daig/omlx-exl3) launches through mx.fast.metal_kernel
+ * (src/omlx/exl3/kernels.py:243-246, 344-351, 446-447) and every MLX built-in on the layer's path
+ * (mx.hadamard_transform and the fp16 matmul of linear.py:31-33, 97-105) has one entry point here.
+ *
+ * Conventions
+ *   - Pointers are device pointers (hipMalloc / torch tensors' data_ptr()), sizes are element counts.
+ *   - `stream` is a hipStream_t (NULL = the default stream). Work is enqueued and the call returns:
+ *     no allocation, no host synchronisation, no implicit stream. Calls are graph-capturable.
+ *   - Return value: 0 on success, a negative EXL3_ERR_* on failure; exl3_last_error() then describes
+ *     the failure (thread-local, valid until the next failing call on that thread).
+ *   - fp16 buffers are IEEE half bit patterns (uint16_t); dtype enums select fp16 / bf16 / fp32.
+ *   - The trellis of a K-bit tensor is the checkpoint's int16 [k/16, n/16, 16K] array, passed as its
+ *     flat little-endian uint32 view (linear.py:69), 4-byte aligned.
+ */
+#ifndef EXL3_MI355X_H
+#define EXL3_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define EXL3_OK 0
+#define EXL3_ERR_ARG (-1)      /* invalid argument (shape, K, codebook, dtype, pointer, alignment) */
+#define EXL3_ERR_WORKSPACE (-2) /* workspace missing or too small */
+#define EXL3_ERR_HIP (-3)      /* a HIP launch or runtime call failed */
+
+#define EXL3_DTYPE_F16 0
+#define EXL3_DTYPE_BF16 1
+#define EXL3_DTYPE_F32 2
+
+#define EXL3_CB_3INST 0
+#define EXL3_CB_MCG 1
+#define EXL3_CB_MUL1 2
+
+#define EXL3_MAX_GEMV_ROWS 16   /* rows one GEMV launch accepts (the reference caps at 8, kernels.py:260) */
+#define EXL3_MAX_MEMBERS 3      /* sibling-group members per GEMV launch (kernels.py:270) */
+
+/* GEMV flags */
+#define EXL3_GEMV_EXACT 0u      /* contract fp16-rounded codebook values (the reference's arithmetic) */
+#define EXL3_GEMV_FAST 1u       /* 3INST/MCG: contract the two fp16 summands of each codebook value
+                                   separately (the unrounded value), one VALU op less per weight */
+
+/* Library version, (major << 16) | (minor << 8) | patch. */
+int exl3_version(void);
+
+/* Description of the last failure on the calling thread ("" if none). */
+const char* exl3_last_error(void);
+
+/* Codebook diagnostic: out[s] = fp16 bits of the codebook value of state s, s = 0..65535, evaluated by
+ * the same device code the GEMV and reconstruct kernels use (state read from the low half of a word
+ * when `hi_half` is 0, from the high half otherwise). Replaces the reference's dec1<CB>
+ * (kernels.py:35-48) as a testable unit. out: uint16[65536]. */
+int exl3_codebook(int cb, int hi_half, uint16_t* out, void* stream);
+
+/* Trellis -> W_inner^T, columns [16*nt0, 16*(nt0+ntc)) of W_inner as a (16*ntc, k) fp16 matrix, bit-exact.
+ * Replaces decode_wt (kernels.py:304-351). trellis: uint32 view of int16 [k/16, n/16, 16K];
+ * w_out: uint16[16*ntc*k]. k % 16 == 0, n % 16 == 0, 1 <= K <= 8, cb in {0,1,2},
+ * 0 <= nt0, ntc >= 1, nt0 + ntc <= n/16. */
+int exl3_reconstruct(const uint32_t* trellis, int k, int n, int K, int cb, int nt0, int ntc,
+                     uint16_t* w_out, void* stream);
+
+/* Workspace bytes exl3_gemv needs for this shape (deterministic split-K partials + per-block arrival
+ * counters). The workspace must be zero-filled once before its first use; every call leaves the
+ * counters at zero again. One workspace must not be used by two calls in flight at the same time. */
+size_t exl3_gemv_workspace_bytes(int k, int n_total, int rows, int K);
+
+/* Fused decode GEMV: y = had128(xh_m @ W_inner_m) * svh (+ bias) for 1..3 sibling members sharing k, K
+ * and codebook, one launch. Replaces TrellisGemvPlan.__call__ (kernels.py:263-299) and its kernel
+ * (kernels.py:114-209), plus the bias add of linear.py:94-95.
+ *   xh       fp16 (n_members, rows, k): each member's rotated input (member-major)
+ *   trellis  n_members pointers, member m: uint32 view of int16 [k/16, member_n[m]/16, 16K]
+ *   member_n output features per member, each % 128 == 0; n_total = sum
+ *   svh      fp16 [n_total]; bias: NULL or [n_total] in out_dtype
+ *   y        (rows, n_total) in out_dtype (EXL3_DTYPE_F16 / BF16 / F32)
+ *   rows     1..EXL3_MAX_GEMV_ROWS; flags: EXL3_GEMV_EXACT or EXL3_GEMV_FAST
+ * Split-K partials are reduced in a fixed order: results are bitwise reproducible run to run, and
+ * row r of the output does not depend on the row count. */
+int exl3_gemv(const uint16_t* xh, const uint32_t* const* trellis, int n_members, const int* member_n,
+              int k, int K, int cb, const uint16_t* svh, const void* bias, void* y, int out_dtype, int rows,
+              unsigned flags, void* workspace, size_t workspace_bytes, void* stream);
+
+/* exl3_gemv with an explicit split-K granularity: kt_per_split k-tiles (16 k each, rounded up to a
+ * multiple of 4) per workgroup, 0 = automatic (what exl3_gemv uses). For tuning sweeps; the workspace
+ * must hold blocks*4 bytes (rounded up to 256) + S*rows*n_total*4 bytes when S = ceil((k/16)/kt_per_split) > 1.
+ * Same role as the reference's pick_tgk override (kernels.py:250-257). */
+int exl3_gemv_ex(const uint16_t* xh, const uint32_t* const* trellis, int n_members, const int* member_n,
+                 int k, int K, int cb, const uint16_t* svh, const void* bias, void* y, int out_dtype, int rows,
+                 unsigned flags, void* workspace, size_t workspace_bytes, int kt_per_split, void* stream);
+
+/* Input rotation: xh[m, r, :] = fp16(H128(x[r, :] * suh[m, :]) / sqrt(128)) per 128-block, fp32 inside.
+ * Replaces rot (kernels.py:388-406, 451-458). x (rows, k) in x_dtype; suh fp16 (n_members, k);
+ * xh fp16 (n_members, rows, k). k % 128 == 0. */
+int exl3_rotate(const void* x, int x_dtype, const uint16_t* suh, int n_members, int rows, int k, uint16_t* xh,
+                void* stream);
+
+/* Fused residual add + RMSNorm + input rotations. Replaces norm_rot (kernels.py:408-425, 461-473) and
+ * the residual add the reference leaves to the model graph.
+ *   h  = T(x + residual)   when residual != NULL (written to residual_out if non-NULL), else h = x
+ *   xn = T(w * T(h * rsqrt(mean(h^2) + eps)))                       (MLX's rounding of rms_norm)
+ *   xh[m] = fp16(H128(xn * suh[m]) / sqrt(128))                     (skipped when n_members == 0)
+ * x, residual, residual_out, w, xn: (rows, k) / (k) in dtype T = EXL3_DTYPE_F16 or BF16;
+ * suh fp16 (n_members, k); xh fp16 (n_members, rows, k). k % 128 == 0. */
+int exl3_rmsnorm_rotate(const void* x, const void* residual, void* residual_out, const void* w, int dtype,
+                        float eps, const uint16_t* suh, int n_members, int rows, int k, void* xn, uint16_t* xh,
+                        void* stream);
+
+/* Fused SwiGLU + rotation: xh[r, :] = fp16(H128(silu(gate) * up * suh) / sqrt(128)), gu = [gate | up].
+ * Replaces swiglu_rot (kernels.py:427-433, 476-483). gu fp16 (rows, 2n); suh fp16 (n); xh fp16 (rows, n).
+ * n % 128 == 0. */
+int exl3_swiglu_rotate(const uint16_t* gu, const uint16_t* suh, int rows, int n, uint16_t* xh, void* stream);
+
+/* Prefill contraction: y = had128(xh @ W_inner) * svh (+ bias) for many rows, with trellis tiles
+ * reconstructed to fp16 inside the kernel (LDS) and contracted on MFMA with fp32 accumulation.
+ * Replaces EXL3Linear._prefill (linear.py:97-105: decode_wt + MLX matmul + hadamard + svh).
+ *   xh fp16 (rows, k) (already rotated); trellis as in exl3_gemv; svh fp16 [n]; bias NULL or [n]
+ *   y (rows, n) in out_dtype. k % 16 == 0, n % 128 == 0, rows >= 1. */
+int exl3_prefill_gemm(const uint16_t* xh, const uint32_t* trellis, int k, int n, int K, int cb,
+                      const uint16_t* svh, const void* bias, void* y, int out_dtype, int rows, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EXL3_MI355X_H */

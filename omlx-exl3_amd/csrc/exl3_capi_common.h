@@ -1,0 +1,37 @@
+// SPDX-License-Identifier: Apache-2.0
+// Host-side helpers shared by the C-ABI entry points: status codes, the thread-local error message and
+// argument checks. Every entry point validates its arguments, launches on the caller's stream and
+// returns 0 or a negative status; it never allocates and never synchronises.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include "../../include/exl3_mi355x.h"
+
+namespace exl3 {
+
+void set_error(const char* fmt, ...);
+
+#define EXL3_REQUIRE(cond, code, ...) \
+  do {                                \
+    if (!(cond)) {                    \
+      ::exl3::set_error(__VA_ARGS__); \
+      return (code);                  \
+    }                                 \
+  } while (0)
+
+#define EXL3_LAUNCH_CHECK(what)                                                             \
+  do {                                                                                      \
+    hipError_t _e = hipGetLastError();                                                      \
+    if (_e != hipSuccess) {                                                                 \
+      ::exl3::set_error("%s: launch failed: %s", (what), hipGetErrorString(_e));            \
+      return EXL3_ERR_HIP;                                                                  \
+    }                                                                                       \
+  } while (0)
+
+inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+}  // namespace exl3

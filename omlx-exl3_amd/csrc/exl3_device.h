@@ -1,0 +1,212 @@
+// SPDX-License-Identifier: Apache-2.0
+// Device-side building blocks for the EXL3 (trellis) kernels on gfx950 (MI355X, CDNA4, wave64).
+//
+// Format (reference src/omlx/exl3/kernels.py:4-8): tile (kt, nt) of a K-bit tensor is 8K little-endian
+// uint32 words at word offset (kt*NT + nt)*8K of the flat trellis. Its 256K-bit stream is read MSB-first;
+// position t's 16-bit state is stream bits [(t+1)K-16, (t+1)K) mod 256K. Run g (positions 32g..32g+31)
+// reads words [Kg, Kg+K) plus the word before it (tail-biting: word 8K-1 for g = 0) and covers tile
+// columns g ("lo", p%8 < 4) and 8+g ("hi"), with k_in = 2*(p/8) + p%2 + 8*((p%4)/2)
+// (kernels.py:52-55, 216, 332).
+//
+// Codebook value of a state s (kernels.py:35-48): h = s*MUL + ADD (mod 2^32), then
+//   3INST / MCG: u = (h & 0x8FFF8FFF) ^ 0x3B603B60, w = f16(u.lo) + f16(u.hi) (one RNE rounding)
+//   MUL1:        r = f16 bits (0x6400 + bytesum(h)) = 1024 + bytesum(h), w = fma_f16(r, 0x1EEE, 0xC931)
+//
+// The hash is evaluated as two full-rate 16-bit multiplies instead of a quarter-rate 32-bit one:
+//   t = s * MUL_lo + ADD                     (v_mad_u32_u16, 32-bit result)
+//   h = t + ((s * MUL_hi) << 16)             (v_pk_mad_u16: low lane t.lo + s*0, high lane t.hi + s*MUL_hi)
+// Both read only 16 bits of their state operand (low or high half by op_sel), so a window needs no
+// masking: a shift (or funnel shift) that puts it in either half is enough, and windows that already sit
+// at bit 0 or bit 16 of a word need no instruction at all.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <type_traits>
+
+namespace exl3 {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kHadScale = 0.08838834764831845f;   // 1/sqrt(128) as the reference rounds it (kernels.py:207)
+
+template <int CB>
+struct Codebook;
+template <>
+struct Codebook<0> {   // 3INST
+  static constexpr uint32_t mul = 89226354u, add = 64248484u;
+};
+template <>
+struct Codebook<1> {   // MCG
+  static constexpr uint32_t mul = 0xCBAC1FEDu, add = 0u;
+};
+template <>
+struct Codebook<2> {   // MUL1
+  static constexpr uint32_t mul = 0x83DCD12Du, add = 0u;
+};
+
+constexpr uint32_t kMask3 = 0x8FFF8FFFu, kXor3 = 0x3B603B60u;
+constexpr uint16_t kMul1Inv = 0x1EEE, kMul1Bias = 0xC931;
+
+// ------------------------------------------------------------------------------------------------
+// compile-time iteration
+// ------------------------------------------------------------------------------------------------
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<I + 1, N>(f);
+  }
+}
+
+// Window geometry of position P (0..31) of a run at K bits per weight: the window ends at local bit
+// e = (P+1)K inside local word ih (0..K-1; -1 is the word before the run), right-shift sh.
+template <int K, int P>
+struct Win {
+  static constexpr int e = (P + 1) * K;
+  static constexpr int ih = (e - 1) / 32;
+  static constexpr int sh = 32 * (ih + 1) - e;
+  static constexpr bool at_lo = sh == 0;        // state = low half of word ih
+  static constexpr bool at_hi = sh == 16;       // state = high half of word ih
+  static constexpr bool inside = sh < 16;       // state = (word ih >> sh), low half
+  // else: funnel of word ih-1 (or the previous run's last word) and word ih
+  static constexpr int k_in = 2 * (P / 8) + (P % 2) + 8 * ((P % 4) / 2);
+  static constexpr bool hi_col = (P % 8) >= 4;
+};
+
+// ------------------------------------------------------------------------------------------------
+// hash: h = s*MUL + ADD for the 16-bit state held in the low (HI=false) or high (HI=true) half of src
+// ------------------------------------------------------------------------------------------------
+template <int CB, bool HI>
+__device__ __forceinline__ uint32_t hash16(uint32_t src) {
+  constexpr uint32_t mlo = Codebook<CB>::mul & 0xFFFFu;
+  constexpr uint32_t mhi16 = Codebook<CB>::mul & 0xFFFF0000u;   // MUL_hi in the high lane, 0 in the low lane
+  uint32_t t, h;
+  if constexpr (Codebook<CB>::add != 0) {
+    const uint32_t add = Codebook<CB>::add;
+    if constexpr (HI)
+      asm("v_mad_u32_u16 %0, %1, %2, %3 op_sel:[1,0,0,0]" : "=v"(t) : "v"(src), "s"(mlo), "v"(add));
+    else
+      asm("v_mad_u32_u16 %0, %1, %2, %3" : "=v"(t) : "v"(src), "s"(mlo), "v"(add));
+  } else {
+    if constexpr (HI)
+      asm("v_mad_u32_u16 %0, %1, %2, 0 op_sel:[1,0,0,0]" : "=v"(t) : "v"(src), "s"(mlo));
+    else
+      asm("v_mad_u32_u16 %0, %1, %2, 0" : "=v"(t) : "v"(src), "s"(mlo));
+  }
+  if constexpr (HI)
+    asm("v_pk_mad_u16 %0, %1, %2, %3" : "=v"(h) : "v"(src), "s"(mhi16), "v"(t));
+  else
+    asm("v_pk_mad_u16 %0, %1, %2, %3 op_sel_hi:[0,1,1]" : "=v"(h) : "v"(src), "s"(mhi16), "v"(t));
+  return h;
+}
+
+// State source of position P from the run's words w[0..K-1] and the word before the run (wp):
+// returns a register whose low half (or high half, when Win::at_hi) is the 16-bit state.
+template <int K, int P>
+__device__ __forceinline__ uint32_t window_src(const uint32_t* w, uint32_t wp) {
+  using W = Win<K, P>;
+  if constexpr (W::at_lo || W::at_hi) {
+    return w[W::ih];
+  } else if constexpr (W::inside) {
+    return w[W::ih] >> W::sh;
+  } else {
+    const uint32_t prev = W::ih > 0 ? w[W::ih > 0 ? W::ih - 1 : 0] : wp;
+    return __builtin_amdgcn_alignbit(prev, w[W::ih], W::sh);
+  }
+}
+
+template <int CB, int K, int P>
+__device__ __forceinline__ uint32_t hash_pos(const uint32_t* w, uint32_t wp) {
+  return hash16<CB, Win<K, P>::at_hi>(window_src<K, P>(w, wp));
+}
+
+// 3INST / MCG: the two fp16 summands of the codebook value as one packed register (a in low, b in high)
+__device__ __forceinline__ uint32_t split_pair(uint32_t h) { return (h & kMask3) ^ kXor3; }
+
+// 3INST / MCG: fp16(a0 + b0) in the low half and fp16(a1 + b1) in the high half (one RNE rounding each)
+__device__ __forceinline__ uint32_t sum_pairs(uint32_t u0, uint32_t u1) {
+  uint32_t d;
+  asm("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1\n\t"
+      "v_add_f16_sdwa %0, %2, %2 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_1"
+      : "=&v"(d)
+      : "v"(u0), "v"(u1));
+  return d;
+}
+
+// MUL1: 0x6400 + bytesum(h) (the fp16 bits of 1024 + S) in the low half, zero high half
+__device__ __forceinline__ uint32_t mul1_r(uint32_t h) { return __builtin_amdgcn_sad_u8(h, 0u, 0x6400u); }
+
+// MUL1: fma_f16(r, inv, bias) for two packed r values (one rounding each)
+__device__ __forceinline__ uint32_t mul1_pair(uint32_t r0, uint32_t r1) {
+  const uint32_t r = (r1 << 16) | r0;
+  f16x2 rv = __builtin_bit_cast(f16x2, r);
+  const f16x2 inv = __builtin_bit_cast(f16x2, (uint32_t)kMul1Inv * 0x10001u);
+  const f16x2 bias = __builtin_bit_cast(f16x2, (uint32_t)kMul1Bias * 0x10001u);
+  f16x2 w = __builtin_elementwise_fma(rv, inv, bias);
+  return __builtin_bit_cast(uint32_t, w);
+}
+
+// Codebook value of one state as fp16 bits (scalar path for the reconstruct kernel).
+template <int CB>
+__device__ __forceinline__ uint16_t dec_one(uint32_t h) {
+  if constexpr (CB == 2) {
+    const uint32_t r = mul1_r(h);
+    const float w = __builtin_fmaf(static_cast<float>(__builtin_bit_cast(_Float16, (uint16_t)r)),
+                                   static_cast<float>(__builtin_bit_cast(_Float16, kMul1Inv)),
+                                   static_cast<float>(__builtin_bit_cast(_Float16, kMul1Bias)));
+    // (1024+S)*inv + bias is exact in fp32, so this single rounding equals the fused fp16 fma
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(w));
+  } else {
+    const uint32_t u = split_pair(h);
+    const _Float16 a = __builtin_bit_cast(_Float16, (uint16_t)(u & 0xFFFFu));
+    const _Float16 b = __builtin_bit_cast(_Float16, (uint16_t)(u >> 16));
+    return __builtin_bit_cast(uint16_t, (_Float16)(a + b));
+  }
+}
+
+// ------------------------------------------------------------------------------------------------
+// float <-> 16-bit storage types
+// ------------------------------------------------------------------------------------------------
+enum DType : int { kF16 = 0, kBF16 = 1, kF32 = 2 };
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __builtin_bit_cast(float, (uint32_t)b << 16); }
+
+__device__ __forceinline__ uint16_t f32_to_bf16(float v) {   // round to nearest even, NaN kept quiet
+  uint32_t u = __builtin_bit_cast(uint32_t, v);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float f16_to_f32(uint16_t b) { return (float)__builtin_bit_cast(_Float16, b); }
+__device__ __forceinline__ uint16_t f32_to_f16(float v) { return __builtin_bit_cast(uint16_t, (_Float16)v); }
+
+template <int DT>
+__device__ __forceinline__ float load_as_f32(const void* p, size_t i) {
+  if constexpr (DT == kF16) return f16_to_f32(static_cast<const uint16_t*>(p)[i]);
+  else if constexpr (DT == kBF16) return bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
+  else return static_cast<const float*>(p)[i];
+}
+
+template <int DT>
+__device__ __forceinline__ void store_from_f32(void* p, size_t i, float v) {
+  if constexpr (DT == kF16) static_cast<uint16_t*>(p)[i] = f32_to_f16(v);
+  else if constexpr (DT == kBF16) static_cast<uint16_t*>(p)[i] = f32_to_bf16(v);
+  else static_cast<float*>(p)[i] = v;
+}
+
+// Round through the storage type T (fp16 / bf16 / fp32 identity).
+template <int DT>
+__device__ __forceinline__ float round_through(float v) {
+  if constexpr (DT == kF16) return f16_to_f32(f32_to_f16(v));
+  else if constexpr (DT == kBF16) return bf16_to_f32(f32_to_bf16(v));
+  else return v;
+}
+
+}  // namespace exl3

@@ -1,0 +1,145 @@
+// SPDX-License-Identifier: Apache-2.0
+// Trellis -> fp16 weights, bit-exact (replaces decode_wt, reference src/omlx/exl3/kernels.py:304-351),
+// the codebook diagnostic, and the library's version / error entry points.
+//
+// Reconstruct: one thread per (output column pair, k-tile) run: it reads the run's K stream words plus the
+// word before, decodes 32 weights (columns g and 8+g of the tile, all 16 k) and writes two contiguous
+// 32-byte row segments of W_inner^T. Threads are ordered k-tile fastest, so a wavefront writes 64
+// consecutive segments of the same two output rows (2 KiB contiguous each): the kernel is bound by its
+// 2 bytes/weight of HBM writes (plus K/8 bytes/weight of reads).
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "exl3_capi_common.h"
+#include "exl3_device.h"
+
+namespace exl3 {
+
+static thread_local char g_error[512];
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_error, sizeof(g_error), fmt, ap);
+  va_end(ap);
+}
+
+template <int K, int CB>
+__global__ __launch_bounds__(256) void reconstruct_kernel(const uint32_t* __restrict__ tr, int KT, int NT, int nt0,
+                                                          int ntc, uint16_t* __restrict__ w) {
+  constexpr int TW = 8 * K;
+  const size_t gid = (size_t)blockIdx.x * 256 + threadIdx.x;
+  const size_t total = (size_t)ntc * 8 * KT;
+  if (gid >= total) return;
+  const int kt = (int)(gid % (size_t)KT);
+  const int rg = (int)(gid / (size_t)KT);
+  const int g = rg & 7, ntl = rg >> 3;
+  const uint32_t* tp = tr + ((size_t)kt * NT + nt0 + ntl) * TW;
+  uint32_t wv[K];
+#pragma unroll
+  for (int i = 0; i < K; ++i) wv[i] = tp[K * g + i];
+  const uint32_t wp = tp[(K * g + TW - 1) % TW];
+
+  uint32_t lo[8] = {}, hi[8] = {};
+  static_for<0, 32>([&](auto P) {
+    constexpr int p = decltype(P)::value;
+    using W = Win<K, p>;
+    const uint16_t v = dec_one<CB>(hash_pos<CB, K, p>(wv, wp));
+    uint32_t* dst = W::hi_col ? hi : lo;
+    dst[W::k_in >> 1] |= (uint32_t)v << (16 * (W::k_in & 1));
+  });
+  const size_t kk = (size_t)KT * 16;
+  u32x4* wlo = reinterpret_cast<u32x4*>(w + ((size_t)ntl * 16 + g) * kk + (size_t)kt * 16);
+  u32x4* whi = reinterpret_cast<u32x4*>(w + ((size_t)ntl * 16 + 8 + g) * kk + (size_t)kt * 16);
+  wlo[0] = u32x4{lo[0], lo[1], lo[2], lo[3]};
+  wlo[1] = u32x4{lo[4], lo[5], lo[6], lo[7]};
+  whi[0] = u32x4{hi[0], hi[1], hi[2], hi[3]};
+  whi[1] = u32x4{hi[4], hi[5], hi[6], hi[7]};
+}
+
+// All 65,536 states through the GEMV's exact decode path (hash16 from either half of a register, then
+// the packed fp16 pair sum or the packed MUL1 fma). The unused half of each source register holds junk
+// bits, which the 16-bit hash operands must ignore.
+template <int CB, bool HI>
+__global__ __launch_bounds__(256) void codebook_kernel(uint16_t* __restrict__ out) {
+  const uint32_t i = blockIdx.x * 256 + threadIdx.x;   // pair index, 0..32767
+  const uint32_t s0 = 2 * i, s1 = 2 * i + 1;
+  const uint32_t junk0 = (s0 * 0x9E3779B9u) >> 16, junk1 = (s1 * 0x85EBCA6Bu) >> 16;
+  const uint32_t src0 = HI ? (s0 << 16) | junk0 : s0 | (junk0 << 16);
+  const uint32_t src1 = HI ? (s1 << 16) | junk1 : s1 | (junk1 << 16);
+  const uint32_t h0 = hash16<CB, HI>(src0), h1 = hash16<CB, HI>(src1);
+  uint32_t d;
+  if constexpr (CB == 2) d = mul1_pair(mul1_r(h0), mul1_r(h1));
+  else d = sum_pairs(split_pair(h0), split_pair(h1));
+  out[s0] = (uint16_t)(d & 0xFFFFu);
+  out[s1] = (uint16_t)(d >> 16);
+}
+
+template <int K, int CB>
+static void launch_reconstruct(const uint32_t* tr, int KT, int NT, int nt0, int ntc, uint16_t* w, hipStream_t st) {
+  const size_t total = (size_t)ntc * 8 * KT;
+  const unsigned blocks = (unsigned)((total + 255) / 256);
+  reconstruct_kernel<K, CB><<<blocks, 256, 0, st>>>(tr, KT, NT, nt0, ntc, w);
+}
+
+template <int CB>
+static void dispatch_reconstruct_k(int K, const uint32_t* tr, int KT, int NT, int nt0, int ntc, uint16_t* w,
+                                   hipStream_t st) {
+  switch (K) {
+    case 1: launch_reconstruct<1, CB>(tr, KT, NT, nt0, ntc, w, st); break;
+    case 2: launch_reconstruct<2, CB>(tr, KT, NT, nt0, ntc, w, st); break;
+    case 3: launch_reconstruct<3, CB>(tr, KT, NT, nt0, ntc, w, st); break;
+    case 4: launch_reconstruct<4, CB>(tr, KT, NT, nt0, ntc, w, st); break;
+    case 5: launch_reconstruct<5, CB>(tr, KT, NT, nt0, ntc, w, st); break;
+    case 6: launch_reconstruct<6, CB>(tr, KT, NT, nt0, ntc, w, st); break;
+    case 7: launch_reconstruct<7, CB>(tr, KT, NT, nt0, ntc, w, st); break;
+    default: launch_reconstruct<8, CB>(tr, KT, NT, nt0, ntc, w, st); break;
+  }
+}
+
+}  // namespace exl3
+
+using namespace exl3;
+
+extern "C" int exl3_version(void) { return (0 << 16) | (1 << 8) | 0; }
+
+extern "C" const char* exl3_last_error(void) { return g_error; }
+
+extern "C" int exl3_codebook(int cb, int hi_half, uint16_t* out, void* stream) {
+  EXL3_REQUIRE(cb >= 0 && cb <= 2, EXL3_ERR_ARG, "exl3_codebook: codebook must be 0, 1 or 2 (got %d)", cb);
+  EXL3_REQUIRE(out != nullptr, EXL3_ERR_ARG, "exl3_codebook: out is NULL");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const unsigned blocks = 32768 / 256;
+  if (hi_half) {
+    if (cb == 0) codebook_kernel<0, true><<<blocks, 256, 0, st>>>(out);
+    else if (cb == 1) codebook_kernel<1, true><<<blocks, 256, 0, st>>>(out);
+    else codebook_kernel<2, true><<<blocks, 256, 0, st>>>(out);
+  } else {
+    if (cb == 0) codebook_kernel<0, false><<<blocks, 256, 0, st>>>(out);
+    else if (cb == 1) codebook_kernel<1, false><<<blocks, 256, 0, st>>>(out);
+    else codebook_kernel<2, false><<<blocks, 256, 0, st>>>(out);
+  }
+  EXL3_LAUNCH_CHECK("exl3_codebook");
+  return EXL3_OK;
+}
+
+extern "C" int exl3_reconstruct(const uint32_t* trellis, int k, int n, int K, int cb, int nt0, int ntc,
+                                uint16_t* w_out, void* stream) {
+  EXL3_REQUIRE(trellis && w_out, EXL3_ERR_ARG, "exl3_reconstruct: NULL pointer");
+  EXL3_REQUIRE(k > 0 && n > 0 && k % 16 == 0 && n % 16 == 0, EXL3_ERR_ARG,
+               "exl3_reconstruct: k and n must be positive multiples of 16 (k=%d, n=%d)", k, n);
+  EXL3_REQUIRE(K >= 1 && K <= 8, EXL3_ERR_ARG, "exl3_reconstruct: K must be 1..8 (got %d)", K);
+  EXL3_REQUIRE(cb >= 0 && cb <= 2, EXL3_ERR_ARG, "exl3_reconstruct: codebook must be 0, 1 or 2 (got %d)", cb);
+  EXL3_REQUIRE(nt0 >= 0 && ntc >= 1 && nt0 + ntc <= n / 16, EXL3_ERR_ARG,
+               "exl3_reconstruct: column window [%d, %d) outside 0..%d tiles", nt0, nt0 + ntc, n / 16);
+  EXL3_REQUIRE(aligned(trellis, 4) && aligned(w_out, 16), EXL3_ERR_ARG,
+               "exl3_reconstruct: trellis must be 4-byte and w_out 16-byte aligned");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int KT = k / 16, NT = n / 16;
+  if (cb == 0) dispatch_reconstruct_k<0>(K, trellis, KT, NT, nt0, ntc, w_out, st);
+  else if (cb == 1) dispatch_reconstruct_k<1>(K, trellis, KT, NT, nt0, ntc, w_out, st);
+  else dispatch_reconstruct_k<2>(K, trellis, KT, NT, nt0, ntc, w_out, st);
+  EXL3_LAUNCH_CHECK("exl3_reconstruct");
+  return EXL3_OK;
+}

@@ -1,0 +1,200 @@
+# SPDX-License-Identifier: Apache-2.0
+"""Host-side wrappers of the HIP kernels, mirroring the reference's kernel API
+(src/omlx/exl3/kernels.py): decode_wt, rot, norm_rot, swiglu_rot, TrellisGemvPlan, MAX_GEMV_ROWS, plus
+prefill_gemm (the fused replacement of decode_wt + matmul + Hadamard on the prefill path) and codebook
+(the codebook diagnostic).
+
+Tensors are torch tensors on the HIP device; every call is enqueued on torch's current stream and returns
+without synchronising. Argument errors raise before anything is launched (the reference asserts,
+kernels.py:269-270, 465); the C library re-validates and its status becomes an Exl3Error.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from ._capi import DTYPE_CODE, Exl3Error, check, lib, ptr, stream_handle
+
+MAX_GEMV_ROWS = 8           # rows at or below which EXL3Linear takes the GEMV path (kernels.py:260)
+GEMV_ROWS_LIMIT = 16        # rows one GEMV launch accepts
+GEMV_EXACT, GEMV_FAST = 0, 1
+
+
+def _require(cond: bool, msg: str) -> None:
+    if not cond:
+        raise ValueError(msg)
+
+
+def _dev(t: torch.Tensor, name: str) -> None:
+    _require(isinstance(t, torch.Tensor) and t.is_cuda, f"{name} must be a tensor on the HIP device")
+    _require(t.is_contiguous(), f"{name} must be contiguous")
+
+
+def trellis_words(trellis: torch.Tensor, k: int, n: int, K: int) -> torch.Tensor:
+    """Check a trellis tensor (int16 [k/16, n/16, 16K], or any contiguous tensor of those bytes)."""
+    _dev(trellis, "trellis")
+    nbytes = trellis.numel() * trellis.element_size()
+    _require(nbytes == k * n * K // 8, f"trellis holds {nbytes} bytes, expected k*n*K/8 = {k * n * K // 8}")
+    return trellis
+
+
+def codebook(cb: int, hi_half: bool = False, device=None) -> torch.Tensor:
+    """All 65,536 codebook values (fp16) through the kernels' decode path."""
+    out = torch.empty(65536, dtype=torch.float16, device=device or "cuda")
+    check(lib().exl3_codebook(cb, int(hi_half), ptr(out), stream_handle(out.device)), "exl3_codebook")
+    return out
+
+
+def decode_wt(trellis: torch.Tensor, k: int, n: int, K: int, cb: int, nt0: int = 0, ntc: int | None = None,
+              out: torch.Tensor | None = None) -> torch.Tensor:
+    """W_inner^T columns [16*nt0, 16*(nt0+ntc)) as a (16*ntc, k) fp16 matrix (kernels.py:340-351)."""
+    ntc = n // 16 - nt0 if ntc is None else ntc
+    _require(k % 16 == 0 and n % 16 == 0 and 1 <= K <= 8 and cb in (0, 1, 2), "bad k, n, K or codebook")
+    trellis_words(trellis, k, n, K)
+    if out is None:
+        out = torch.empty((16 * ntc, k), dtype=torch.float16, device=trellis.device)
+    _require(out.dtype == torch.float16 and out.shape == (16 * ntc, k), "decode_wt: bad output tensor")
+    check(lib().exl3_reconstruct(ptr(trellis), k, n, K, cb, nt0, ntc, ptr(out), stream_handle(trellis.device)),
+          "exl3_reconstruct")
+    return out
+
+
+def rot(x: torch.Tensor, suh: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """x (rows, k) fp16/bf16/fp32, suh (NM, k) fp16 -> xh (NM, rows, k) fp16 (kernels.py:451-458)."""
+    _dev(x, "x")
+    _dev(suh, "suh")
+    rows, k = x.shape
+    suh2 = suh.reshape(-1, k)
+    nm = suh2.shape[0]
+    _require(x.dtype in DTYPE_CODE and suh.dtype == torch.float16, "rot: x must be fp16/bf16/fp32, suh fp16")
+    if out is None:
+        out = torch.empty((nm, rows, k), dtype=torch.float16, device=x.device)
+    check(lib().exl3_rotate(ptr(x), DTYPE_CODE[x.dtype], ptr(suh2), nm, rows, k, ptr(out), stream_handle(x.device)),
+          "exl3_rotate")
+    return out
+
+
+def norm_rot(x: torch.Tensor, w: torch.Tensor, eps: float, suh: torch.Tensor | None,
+             residual: torch.Tensor | None = None, residual_out: torch.Tensor | None = None):
+    """RMSNorm(x [+ residual]) * w in x.dtype (MLX's rounding) and its rotations xh (NM, rows, k) fp16
+    (kernels.py:461-473). With a residual, x + residual is also written to residual_out (allocated when
+    not given) and returned third: (xn, xh, h)."""
+    _dev(x, "x")
+    _dev(w, "w")
+    rows, k = x.shape
+    _require(x.dtype in (torch.float16, torch.bfloat16) and w.dtype == x.dtype, "norm_rot: fp16/bf16 x and w")
+    _require(k % 128 == 0, "norm_rot: k must be a multiple of 128")
+    xn = torch.empty_like(x)
+    nm = 0
+    xh = None
+    if suh is not None:
+        _dev(suh, "suh")
+        suh = suh.reshape(-1, k)
+        nm = suh.shape[0]
+        xh = torch.empty((nm, rows, k), dtype=torch.float16, device=x.device)
+    if residual is not None:
+        _dev(residual, "residual")
+        _require(residual.shape == x.shape and residual.dtype == x.dtype, "norm_rot: residual like x")
+        if residual_out is None:
+            residual_out = torch.empty_like(x)
+    check(lib().exl3_rmsnorm_rotate(ptr(x), ptr(residual), ptr(residual_out), ptr(w), DTYPE_CODE[x.dtype],
+                                    float(eps), ptr(suh), nm, rows, k, ptr(xn), ptr(xh), stream_handle(x.device)),
+          "exl3_rmsnorm_rotate")
+    if residual is not None:
+        return xn, xh, residual_out
+    return xn, xh
+
+
+def swiglu_rot(gu: torch.Tensor, suh: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """gu (rows, 2N) = [gate | up] fp16, suh (N,) fp16 -> had128(silu(gate) * up * suh) / sqrt(128),
+    (1, rows, N) fp16 (kernels.py:476-483)."""
+    _dev(gu, "gu")
+    _dev(suh, "suh")
+    rows, n2 = gu.shape
+    n = n2 // 2
+    _require(gu.dtype == torch.float16 and suh.dtype == torch.float16 and suh.numel() == n, "swiglu_rot: fp16")
+    if out is None:
+        out = torch.empty((1, rows, n), dtype=torch.float16, device=gu.device)
+    check(lib().exl3_swiglu_rotate(ptr(gu), ptr(suh), rows, n, ptr(out), stream_handle(gu.device)),
+          "exl3_swiglu_rotate")
+    return out
+
+
+class TrellisGemvPlan:
+    """y = had128(xh @ W_inner) * svh (+ bias) in out_dtype for one EXL3 linear or a sibling group of
+    <= 3 members sharing K and codebook (kernels.py:263-299). xh is (n_members, rows, k): each member's own
+    rotated input. The plan owns the launch parameters and a zeroed workspace (split-K partials and
+    per-block arrival counters that the kernel leaves at zero)."""
+
+    def __init__(self, k: int, member_ns: list[int], K: int, cb: int, svh: torch.Tensor, rows: int,
+                 out_dtype: torch.dtype = torch.float16, *, fast: bool = False, kt_per_split: int = 0):
+        _require(k % 16 == 0 and all(n % 128 == 0 for n in member_ns) and 1 <= K <= 8 and cb in (0, 1, 2),
+                 "TrellisGemvPlan: k % 16, n % 128, 1 <= K <= 8, codebook 0..2")
+        _require(1 <= len(member_ns) <= 3 and 1 <= rows <= GEMV_ROWS_LIMIT, "TrellisGemvPlan: 1..3 members, rows")
+        _require(out_dtype in DTYPE_CODE, "TrellisGemvPlan: out_dtype fp16, bf16 or fp32")
+        self.k, self.ns, self.n, self.K, self.cb, self.rows = k, list(member_ns), sum(member_ns), K, cb, rows
+        self.out_dtype = out_dtype
+        self.nsub = len(member_ns)
+        self.flags = GEMV_FAST if fast else GEMV_EXACT
+        self.kt_per_split = kt_per_split
+        self.svh = svh.to(torch.float16).reshape(-1).contiguous()
+        _require(self.svh.numel() == self.n, "TrellisGemvPlan: svh must have sum(member_ns) elements")
+        self.device = self.svh.device
+        nbytes = lib().exl3_gemv_workspace_bytes(k, self.n, rows, K)
+        if kt_per_split:
+            KT = k // 16
+            kps = (kt_per_split + 3) // 4 * 4
+            S = (KT + kps - 1) // kps
+            nbytes = max(nbytes, (self.n // 128 * 4 + 255) // 256 * 256 + (S * rows * self.n * 4 if S > 1 else 0))
+        self.workspace = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=self.device)
+        self._ns_c = (ctypes.c_int * 3)(*(list(member_ns) + [0] * (3 - len(member_ns))))
+        self._tr_key = None
+        self._tr_c = None
+
+    def __call__(self, xh: torch.Tensor, trellises: list[torch.Tensor], bias: torch.Tensor | None = None,
+                 out: torch.Tensor | None = None) -> torch.Tensor:
+        """trellises: one per member. Returns (rows, n) in out_dtype."""
+        _dev(xh, "xh")
+        _require(xh.dtype == torch.float16 and xh.numel() == self.nsub * self.rows * self.k,
+                 f"xh must be fp16 ({self.nsub}, {self.rows}, {self.k})")
+        _require(len(trellises) == self.nsub, "one trellis per member")
+        key = tuple(t.data_ptr() for t in trellises)
+        if key != self._tr_key:
+            for t, n in zip(trellises, self.ns):
+                trellis_words(t, self.k, n, self.K)
+            self._tr_c = (ctypes.c_void_p * 3)(*(list(key) + [key[0]] * (3 - len(key))))
+            self._tr_key = key
+            self._tr_refs = list(trellises)
+        if bias is not None:
+            _require(bias.dtype == self.out_dtype and bias.numel() == self.n and bias.is_contiguous(),
+                     "bias must be contiguous, out_dtype, n elements")
+        if out is None:
+            out = torch.empty((self.rows, self.n), dtype=self.out_dtype, device=xh.device)
+        rc = lib().exl3_gemv_ex(ptr(xh), self._tr_c, self.nsub, self._ns_c, self.k, self.K, self.cb, ptr(self.svh),
+                                ptr(bias), ptr(out), DTYPE_CODE[self.out_dtype], self.rows, self.flags,
+                                ptr(self.workspace), self.workspace.numel(), self.kt_per_split,
+                                stream_handle(xh.device))
+        check(rc, "exl3_gemv")
+        return out
+
+
+def prefill_gemm(xh: torch.Tensor, trellis: torch.Tensor, k: int, n: int, K: int, cb: int, svh: torch.Tensor,
+                 bias: torch.Tensor | None = None, out_dtype: torch.dtype = torch.float16,
+                 out: torch.Tensor | None = None) -> torch.Tensor:
+    """had128(xh @ W_inner) * svh (+ bias) for xh (rows, k) fp16 (already rotated), weights reconstructed
+    in LDS and contracted on MFMA (the fused form of linear.py:97-105)."""
+    _dev(xh, "xh")
+    rows = xh.numel() // k
+    _require(xh.dtype == torch.float16 and xh.numel() == rows * k, "xh must be fp16 (rows, k)")
+    trellis_words(trellis, k, n, K)
+    svh = svh.to(torch.float16).reshape(-1).contiguous()
+    if out is None:
+        out = torch.empty((rows, n), dtype=out_dtype, device=xh.device)
+    check(lib().exl3_prefill_gemm(ptr(xh), ptr(trellis), k, n, K, cb, ptr(svh), ptr(bias), ptr(out),
+                                  DTYPE_CODE[out_dtype], rows, stream_handle(xh.device)), "exl3_prefill_gemm")
+    return out
+
+
+__all__ = ["MAX_GEMV_ROWS", "GEMV_ROWS_LIMIT", "TrellisGemvPlan", "decode_wt", "rot", "norm_rot", "swiglu_rot",
+           "prefill_gemm", "codebook", "Exl3Error"]

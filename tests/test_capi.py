@@ -1,0 +1,94 @@
+"""CPU checks of the C ABI: the library loads, exports every function include/exl3_mi355x.h declares, and
+rejects invalid arguments with a negative status and a message before launching anything."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from conftest import ROOT, load_package
+
+HEADER = os.path.join(ROOT, "include", "exl3_mi355x.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(exl3_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def capi():
+    pk = load_package()
+    from omlx_exl3_amd import _capi
+    if not os.path.exists(_capi.LIB_PATH):
+        pytest.skip("library not built")
+    return _capi
+
+
+def test_header_declares_the_entry_points():
+    fns = declared_functions()
+    for name in ("exl3_gemv", "exl3_reconstruct", "exl3_rotate", "exl3_rmsnorm_rotate", "exl3_swiglu_rotate",
+                 "exl3_prefill_gemm", "exl3_gemv_workspace_bytes", "exl3_version", "exl3_last_error"):
+        assert name in fns
+
+
+def test_library_exports_every_declared_symbol(capi):
+    lib = capi.lib()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+    assert set(capi.EXPORTED) >= set(declared_functions())
+    assert lib.exl3_version() >= 0x000100
+
+
+def _err(capi):
+    return capi.lib().exl3_last_error().decode()
+
+
+def test_argument_errors(capi):
+    lib = capi.lib()
+    p = ctypes.c_void_p(0x1000)
+    # reconstruct: bad K, bad k, NULL, window outside
+    assert lib.exl3_reconstruct(p, 64, 64, 9, 0, 0, 4, p, None) == -1 and "K must be" in _err(capi)
+    assert lib.exl3_reconstruct(p, 60, 64, 4, 0, 0, 4, p, None) == -1 and "multiples of 16" in _err(capi)
+    assert lib.exl3_reconstruct(None, 64, 64, 4, 0, 0, 4, p, None) == -1 and "NULL" in _err(capi)
+    assert lib.exl3_reconstruct(p, 64, 64, 4, 0, 2, 3, p, None) == -1 and "window" in _err(capi)
+    assert lib.exl3_reconstruct(p, 64, 64, 4, 3, 0, 4, p, None) == -1 and "codebook" in _err(capi)
+    # gemv: members, n % 128, rows, flags, workspace
+    trs = (ctypes.c_void_p * 3)(0x1000, 0x1000, 0x1000)
+    ns = (ctypes.c_int * 3)(128, 128, 128)
+    args = dict(xh=p, tr=trs, nm=1, ns=ns, k=1024, K=6, cb=0, svh=p, bias=None, y=p, ot=0, rows=1, flags=0,
+                ws=None, wsb=0, st=None)
+
+    def gemv(**kw):
+        a = dict(args, **kw)
+        return lib.exl3_gemv(a["xh"], a["tr"], a["nm"], a["ns"], a["k"], a["K"], a["cb"], a["svh"], a["bias"],
+                             a["y"], a["ot"], a["rows"], a["flags"], a["ws"], a["wsb"], a["st"])
+
+    assert gemv(nm=4) == -1 and "members" in _err(capi)
+    assert gemv(ns=(ctypes.c_int * 3)(100, 0, 0)) == -1 and "multiple of 128" in _err(capi)
+    assert gemv(rows=17) == -1 and "rows" in _err(capi)
+    assert gemv(rows=0) == -1
+    assert gemv(flags=4) == -1 and "flags" in _err(capi)
+    assert gemv(K=0) == -1
+    assert gemv(ot=7) == -1
+    # k=1024 K=6 rows=1 n=128 splits k -> needs a workspace
+    assert gemv() == -2 and "workspace" in _err(capi)
+    assert lib.exl3_gemv_workspace_bytes(1024, 128, 1, 6) > 0
+    assert lib.exl3_gemv_workspace_bytes(1000, 128, 1, 6) == 0
+    # rotations
+    assert lib.exl3_rotate(p, 0, p, 1, 1, 100, p, None) == -1 and "128" in _err(capi)
+    assert lib.exl3_rotate(p, 5, p, 1, 1, 128, p, None) == -1
+    assert lib.exl3_rmsnorm_rotate(p, None, None, p, 2, 1e-6, p, 1, 1, 128, p, p, None) == -1
+    assert lib.exl3_swiglu_rotate(p, p, 1, 100, p, None) == -1
+    assert lib.exl3_prefill_gemm(p, p, 64, 100, 6, 0, p, None, p, 0, 4, None) == -1
+    assert lib.exl3_codebook(3, 0, p, None) == -1
+
+
+def test_package_fails_loudly_without_library(tmp_path, monkeypatch):
+    load_package()
+    from omlx_exl3_amd import _capi
+    monkeypatch.setattr(_capi, "LIB_PATH", str(tmp_path / "missing.so"))
+    monkeypatch.setattr(_capi, "_lib", None)
+    with pytest.raises(_capi.Exl3Error):
+        _capi.lib()

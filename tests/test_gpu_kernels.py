@@ -1,0 +1,271 @@
+"""GPU parity tests of the HIP kernels against the CPU oracle (oracle/exl3_oracle.py), through the C ABI.
+
+Bars: bit-exact for reconstruction, the codebook and the rotations (integer / fully defined fp32
+arithmetic); GEMV and prefill within max-abs-rel 2e-3 (fp16 / fp32 output) or 1e-2 (bf16 output) of an
+fp64 reference, the reference's own bars (exl3_kernel_test.py:50). Full 27B-class shapes are checked
+through size-independent properties: GEMV == (bit-exact reconstruct, fp32 matmul, Hadamard, svh);
+bitwise determinism; row-exactness (row r identical for any row count).
+"""
+import numpy as np
+import pytest
+
+from conftest import load_package
+from oracle import exl3_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+@pytest.fixture(scope="module")
+def pk():
+    return load_package()
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def f16_bits(t):
+    return t.cpu().view(torch.int16).numpy().view(np.uint16)
+
+
+# ------------------------------------------------------------------------------------------ codebook
+@pytest.mark.parametrize("cb", [0, 1, 2])
+@pytest.mark.parametrize("hi", [False, True])
+def test_codebook_bit_exact(pk, cb, hi):
+    got = f16_bits(pk.kernels.codebook(cb, hi_half=hi))
+    assert np.array_equal(got, O.codebook_table(cb))
+
+
+# ------------------------------------------------------------------------------------------ reconstruct
+def test_reconstruct_golden(pk):
+    import os
+    z = np.load(os.path.join(os.path.dirname(__file__), "golden", "exl3_tiles.npz"))
+    for K in range(1, 9):
+        for cb in range(3):
+            tr = dev(z[f"words_K{K}"].view(np.int16).reshape(1, 1, 16 * K))
+            wt = pk.kernels.decode_wt(tr, 16, 16, K, cb)
+            assert np.array_equal(f16_bits(wt).T, z[f"w_K{K}_cb{cb}"]), (K, cb)
+            mt = dev(z[f"multi_words_K{K}"].view(np.int16).reshape(2, 3, 16 * K))
+            wt = pk.kernels.decode_wt(mt, 32, 48, K, cb)
+            assert np.array_equal(f16_bits(wt).T, z[f"multi_w_K{K}_cb{cb}"]), (K, cb)
+
+
+@pytest.mark.parametrize("K", range(1, 9))
+def test_reconstruct_random_all_codebooks(pk, K):
+    k, n = 96, 160
+    tr_np = O.random_trellis(k, n, K, 40 + K)
+    tr = dev(tr_np)
+    for cb in range(3):
+        want = O.reconstruct_inner(tr_np, k, n, K, cb)
+        got = f16_bits(pk.kernels.decode_wt(tr, k, n, K, cb)).T
+        assert np.array_equal(got, want), (K, cb)
+    # column window
+    want = O.decode_wt(tr_np, k, n, K, 1, nt0=3, ntc=4).view(np.uint16)
+    got = f16_bits(pk.kernels.decode_wt(tr, k, n, K, 1, nt0=3, ntc=4))
+    assert np.array_equal(got, want)
+
+
+def test_reconstruct_config1_bit_exact(pk):
+    """4096 x 4096 at K=4, uniform random bits, W bit-exact."""
+    k = n = 4096
+    tr_np = O.random_trellis(k, n, 4, 1)
+    got = f16_bits(pk.kernels.decode_wt(dev(tr_np), k, n, 4, 0)).T
+    assert np.array_equal(got, O.reconstruct_inner(tr_np, k, n, 4, 0))
+
+
+# ------------------------------------------------------------------------------------------ rotations
+@pytest.mark.parametrize("xdt", ["f16", "bf16", "f32"])
+def test_rot_bit_exact(pk, xdt):
+    rng = np.random.default_rng(5)
+    for rows, k, nm in ((1, 5120, 1), (3, 5120, 2), (8, 6144, 3), (2, 17408, 1)):
+        xf = (3 * rng.standard_normal((rows, k))).astype(np.float32)
+        suh = (0.5 * rng.standard_normal((nm, k))).astype(np.float16)
+        if xdt == "f16":
+            x_np = xf.astype(np.float16)
+            x = dev(x_np)
+        elif xdt == "bf16":
+            x_np = O.f32_to_bf16_bits(xf)
+            x = dev(x_np.view(np.int16)).view(torch.bfloat16)
+        else:
+            x_np = xf
+            x = dev(x_np)
+        got = f16_bits(pk.kernels.rot(x, dev(suh)))
+        want = O.rot(x_np, suh).view(np.uint16)
+        assert np.array_equal(got, want), (rows, k, nm)
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("with_res", [False, True])
+def test_norm_rot_bit_exact(pk, bf16, with_res):
+    rng = np.random.default_rng(6)
+    for rows, k, nm in ((1, 5120, 3), (3, 5120, 2), (8, 6144, 1), (2, 17408, 1)):
+        conv = (lambda a: O.f32_to_bf16_bits(a.astype(np.float32))) if bf16 else (lambda a: a.astype(np.float16))
+        x_np = conv(3 * rng.standard_normal((rows, k)))
+        w_np = conv(1 + 0.1 * rng.standard_normal(k))
+        r_np = conv(rng.standard_normal((rows, k)))
+        suh = (0.5 * rng.standard_normal((nm, k))).astype(np.float16)
+        tdt = torch.bfloat16 if bf16 else torch.float16
+
+        def T(a):
+            return dev(a.view(np.int16)).view(tdt) if bf16 else dev(a)
+
+        res = pk.kernels.norm_rot(T(x_np), T(w_np), 1e-6, dev(suh), residual=T(r_np) if with_res else None)
+        xn_w, xh_w, h_w = O.rmsnorm_rotate(x_np, w_np, 1e-6, suh, bf16, residual=r_np if with_res else None)
+        xn = res[0].cpu().view(torch.int16).numpy().view(np.uint16)
+        assert np.array_equal(xn, xn_w.view(np.uint16)), (rows, k, nm)
+        assert np.array_equal(f16_bits(res[1]), xh_w.view(np.uint16))
+        if with_res:
+            assert np.array_equal(res[2].cpu().view(torch.int16).numpy().view(np.uint16), h_w.view(np.uint16))
+
+
+def test_swiglu_rot(pk):
+    rng = np.random.default_rng(7)
+    for rows in (1, 3, 8):
+        n = 17408
+        gu = (2 * rng.standard_normal((rows, 2 * n))).astype(np.float16)
+        suh = (0.5 * rng.standard_normal(n)).astype(np.float16)
+        got = f16_bits(pk.kernels.swiglu_rot(dev(gu), dev(suh)))
+        want = O.swiglu_rotate(gu, suh).view(np.uint16)
+        # exp(-g) rounded to fp32 through the device's fp64 exp: identical except when the fp64 result
+        # sits on an fp32 rounding boundary (never observed); the reference's own bar is 1e-3
+        assert np.mean(got != want) < 1e-5
+        g, u = gu[:, :n].astype(np.float64), gu[:, n:].astype(np.float64)
+        ref = O.had128_f64(g / (1 + np.exp(-g)) * u * suh.astype(np.float64))
+        assert O.max_abs_rel(got.view(np.float16)[0], ref) < 1e-3
+
+
+# ------------------------------------------------------------------------------------------ GEMV
+def _gemv_case(pk, k, ns, K, cb, rows, out_dtype, fast, seed):
+    rng = np.random.default_rng(seed)
+    trs = [O.random_trellis(k, n, K, seed * 10 + i) for i, n in enumerate(ns)]
+    svh = (rng.standard_normal(sum(ns)) * 0.01).astype(np.float16)
+    xh = rng.standard_normal((len(ns), rows, k)).astype(np.float16)
+    ws = [O.reconstruct_inner(t, k, n, K, cb) for t, n in zip(trs, ns)]
+    offs = np.cumsum([0] + list(ns))
+    ref = np.concatenate([O.gemv_ref(xh[m], ws[m], svh[offs[m]:offs[m + 1]]) for m in range(len(ns))], axis=1)
+    plan = pk.kernels.TrellisGemvPlan(k, ns, K, cb, dev(svh), rows, out_dtype, fast=fast)
+    y = plan(dev(xh), [dev(t) for t in trs])
+    return y, ref
+
+
+REF_TEST_CASES = [(6, [256]), (6, [256, 384]), (6, [128, 256, 128]), (5, [256, 128]), (7, [384]),
+                  (8, [128, 128]), (4, [256]), (3, [128])]     # exl3_kernel_test.py:36-37
+
+
+@pytest.mark.parametrize("bits,ns", REF_TEST_CASES)
+@pytest.mark.parametrize("fast", [False, True])
+def test_gemv_reference_matrix(pk, bits, ns, fast):
+    """The reference's own GEMV test matrix: k=1024, MUL1, rows 1/3/8, fp16 and bf16 outputs."""
+    for rows in (1, 3, 8):
+        for dt, bar in ((torch.float16, 2e-3), (torch.bfloat16, 1e-2)):
+            y, ref = _gemv_case(pk, 1024, ns, bits, 2, rows, dt, fast, seed=bits * 7 + rows)
+            assert y.dtype == dt and tuple(y.shape) == (rows, sum(ns))
+            e = O.max_abs_rel(y.float().cpu().numpy(), ref)
+            assert e < bar, (bits, ns, rows, dt, e)
+
+
+@pytest.mark.parametrize("K", range(1, 9))
+@pytest.mark.parametrize("cb", [0, 1])
+@pytest.mark.parametrize("fast", [False, True])
+def test_gemv_all_bitrates_codebooks(pk, K, cb, fast):
+    for rows in (1, 4):
+        y, ref = _gemv_case(pk, 2048, [256, 128], K, cb, rows, torch.float32, fast, seed=K * 3 + cb)
+        e = O.max_abs_rel(y.cpu().numpy(), ref)
+        assert e < 2e-3, (K, cb, rows, e)
+
+
+def test_gemv_config1(pk):
+    """BASELINE config 1 end to end: x -> rot -> GEMV vs the fp64 oracle linear."""
+    k = n = 4096
+    rng = np.random.default_rng(11)
+    tr = O.random_trellis(k, n, 4, 1)
+    su = np.where(rng.integers(0, 2, k) == 1, 1.0, -1.0).astype(np.float16)
+    sv = np.where(rng.integers(0, 2, n) == 1, 1.0, -1.0).astype(np.float16)
+    x = rng.standard_normal((1, k)).astype(np.float16)
+    ref = O.linear_ref(x, tr, k, n, 4, 0, su, sv)
+    xh = pk.kernels.rot(dev(x), dev(su.reshape(1, k)))
+    for fast in (False, True):
+        plan = pk.kernels.TrellisGemvPlan(k, [n], 4, 0, dev(sv), 1, torch.float32, fast=fast)
+        y = plan(xh, [dev(tr)])
+        assert O.max_abs_rel(y.cpu().numpy(), ref) < 2e-3
+
+
+def _had128_t(v):
+    import math
+    H = torch.tensor(O.sylvester(128), dtype=torch.float32, device=v.device) / math.sqrt(128)
+    r, n = v.shape
+    return (v.reshape(r, n // 128, 128) @ H).reshape(r, n)
+
+
+SHAPES_27B = {"q": (5120, [6144]), "kv": (5120, [1024, 1024]), "qkv": (5120, [6144, 1024, 1024]),
+              "o": (6144, [5120]), "gate_up": (5120, [17408, 17408]), "down": (17408, [5120])}
+
+
+@pytest.mark.parametrize("name", list(SHAPES_27B))
+def test_gemv_27b_shapes_vs_reconstruct(pk, name):
+    """Full-size 27B projections at K=6: GEMV == had128(xh @ W) * svh with W from the bit-exact
+    reconstruct kernel and an fp32 matmul; rows 1 and 8; bitwise deterministic; row-exact."""
+    k, ns = SHAPES_27B[name]
+    K, cb = 6, 0
+    g = torch.Generator(device="cuda").manual_seed(len(name))
+    trs = [torch.randint(-32768, 32768, (k // 16, n // 16, 16 * K), dtype=torch.int16, device="cuda", generator=g)
+           for n in ns]
+    svh = (torch.randn(sum(ns), device="cuda", generator=g) * 0.01).half()
+    xh8 = torch.randn((len(ns), 8, k), device="cuda", generator=g).half()
+    Ws = [pk.kernels.decode_wt(t, k, n, K, cb).float() for t, n in zip(trs, ns)]
+    ref = torch.cat([_had128_t(xh8[m].float() @ Ws[m].T) for m in range(len(ns))], dim=1) * svh.float()
+    for fast in (False, True):
+        plan8 = pk.kernels.TrellisGemvPlan(k, ns, K, cb, svh, 8, torch.float32, fast=fast)
+        y8 = plan8(xh8, trs)
+        e = ((y8 - ref).abs().max() / ref.abs().max()).item()
+        assert e < 2e-3, (name, fast, e)
+        assert torch.equal(y8, plan8(xh8, trs))                       # deterministic
+        plan1 = pk.kernels.TrellisGemvPlan(k, ns, K, cb, svh, 1, torch.float32, fast=fast)
+        y1 = plan1(xh8[:, :1].contiguous(), trs)
+        assert torch.equal(y1[0], y8[0])                              # row-exact
+
+
+def test_gemv_bias_and_split_override(pk):
+    k, n, K = 2048, 512, 6
+    rng = np.random.default_rng(3)
+    tr = O.random_trellis(k, n, K, 2)
+    svh = (rng.standard_normal(n) * 0.01).astype(np.float16)
+    bias = (rng.standard_normal(n) * 0.1).astype(np.float16)
+    xh = rng.standard_normal((1, 2, k)).astype(np.float16)
+    w = O.reconstruct_inner(tr, k, n, K, 0)
+    ref = O.gemv_ref(xh[0], w, svh)
+    ys = []
+    for kps in (0, 4, 8, 12, 128):
+        plan = pk.kernels.TrellisGemvPlan(k, [n], K, 0, dev(svh), 2, torch.float16, kt_per_split=kps)
+        y = plan(dev(xh), [dev(tr)], bias=dev(bias))
+        ys.append(y)
+        yb = y.float().cpu().numpy() - bias.astype(np.float32)
+        assert O.max_abs_rel(yb, ref) < 3e-3, kps
+
+
+# ------------------------------------------------------------------------------------------ prefill
+@pytest.mark.parametrize("K,cb", [(6, 0), (4, 1), (3, 2), (8, 0)])
+def test_prefill_vs_oracle(pk, K, cb):
+    k, n, rows = 512, 384, 200
+    rng = np.random.default_rng(K + cb)
+    tr = O.random_trellis(k, n, K, 9)
+    svh = (rng.standard_normal(n) * 0.01).astype(np.float16)
+    xh = rng.standard_normal((rows, k)).astype(np.float16)
+    ref = O.gemv_ref(xh, O.reconstruct_inner(tr, k, n, K, cb), svh)
+    for dt, bar in ((torch.float16, 2e-3), (torch.float32, 2e-3), (torch.bfloat16, 1e-2)):
+        y = pk.kernels.prefill_gemm(dev(xh), dev(tr), k, n, K, cb, dev(svh), out_dtype=dt)
+        assert O.max_abs_rel(y.float().cpu().numpy(), ref) < bar, (dt,)
+
+
+def test_prefill_27b_shape_vs_reconstruct(pk):
+    k, n, K, rows = 5120, 17408, 6, 512
+    g = torch.Generator(device="cuda").manual_seed(3)
+    tr = torch.randint(-32768, 32768, (k // 16, n // 16, 16 * K), dtype=torch.int16, device="cuda", generator=g)
+    svh = (torch.randn(n, device="cuda", generator=g) * 0.01).half()
+    xh = torch.randn((rows, k), device="cuda", generator=g).half()
+    W = pk.kernels.decode_wt(tr, k, n, K, 0).float()
+    ref = _had128_t(xh.float() @ W.T) * svh.float()
+    y = pk.kernels.prefill_gemm(xh, tr, k, n, K, 0, svh, out_dtype=torch.float32)
+    assert ((y - ref).abs().max() / ref.abs().max()).item() < 2e-3
