@@ -185,7 +185,14 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float v) {   // round to nearest
 }
 
 __device__ __forceinline__ float f16_to_f32(uint16_t b) { return (float)__builtin_bit_cast(_Float16, b); }
-__device__ __forceinline__ uint16_t f32_to_f16(float v) { return __builtin_bit_cast(uint16_t, (_Float16)v); }
+
+// fp32 -> fp16 with round-to-nearest-even from the fp32 value. The empty asm pins the fp32 value: without
+// it the backend folds fptrunc(fmul a, b) into v_fma_mixlo_f16, which rounds the exact product once to fp16
+// instead of rounding it to fp32 first, and so differs from the specified arithmetic on fp32 ties.
+__device__ __forceinline__ uint16_t f32_to_f16(float v) {
+  asm volatile("" : "+v"(v));
+  return __builtin_bit_cast(uint16_t, (_Float16)v);
+}
 
 template <int DT>
 __device__ __forceinline__ float load_as_f32(const void* p, size_t i) {

@@ -98,6 +98,16 @@ __device__ __forceinline__ void load_run(const uint32_t* __restrict__ tp, int g,
 template <typename T>
 __device__ __forceinline__ f16x8 as_f16x8(const T& v) { return __builtin_bit_cast(f16x8, v); }
 
+// The B operands are produced by inline asm, which the compiler's hazard tracking does not count as VALU
+// writes, so it would not insert the wait states an MFMA needs after a VALU write of its source VGPRs.
+// This barrier re-defines the four registers after two wait states (s_nop 1): the MFMA then reads values
+// whose last real writer is at least two instructions back, and the data dependence keeps the decode asm
+// from being scheduled past it.
+__device__ __forceinline__ u32x4 mfma_src(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  asm volatile("s_nop 1" : "+v"(a), "+v"(b), "+v"(c), "+v"(d));
+  return u32x4{a, b, c, d};
+}
+
 template <int K, int CB, bool FAST, int OT>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   constexpr bool SPLIT = FAST && CB < 2;
@@ -166,9 +176,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
         const u32x4 av = reinterpret_cast<const u32x4*>(xrec)[j];
         const f16x8 A = as_f16x8(av);
         acc_lo = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-            A, as_f16x8(u32x4{b[8 * j], b[8 * j + 1], b[8 * j + 2], b[8 * j + 3]}), acc_lo, 0, 0, 0);
+            A, as_f16x8(mfma_src(b[8 * j], b[8 * j + 1], b[8 * j + 2], b[8 * j + 3])), acc_lo, 0, 0, 0);
         acc_hi = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-            A, as_f16x8(u32x4{b[8 * j + 4], b[8 * j + 5], b[8 * j + 6], b[8 * j + 7]}), acc_hi, 0, 0, 0);
+            A, as_f16x8(mfma_src(b[8 * j + 4], b[8 * j + 5], b[8 * j + 6], b[8 * j + 7])), acc_hi, 0, 0, 0);
       }
     } else {
       uint32_t b[16];
@@ -179,9 +189,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
         // positions 16jj + 4half + {0..3} and 16jj + 8 + 4half + {0..3}: registers (8jj + 2half + {0,1}),
         // (8jj + 4 + 2half + {0,1})
         acc_lo = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-            A, as_f16x8(u32x4{b[8 * jj], b[8 * jj + 1], b[8 * jj + 4], b[8 * jj + 5]}), acc_lo, 0, 0, 0);
+            A, as_f16x8(mfma_src(b[8 * jj], b[8 * jj + 1], b[8 * jj + 4], b[8 * jj + 5])), acc_lo, 0, 0, 0);
         acc_hi = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-            A, as_f16x8(u32x4{b[8 * jj + 2], b[8 * jj + 3], b[8 * jj + 6], b[8 * jj + 7]}), acc_hi, 0, 0, 0);
+            A, as_f16x8(mfma_src(b[8 * jj + 2], b[8 * jj + 3], b[8 * jj + 6], b[8 * jj + 7])), acc_hi, 0, 0, 0);
       }
     }
   };
@@ -284,16 +294,20 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
 // ------------------------------------------------------------------------------------------------
 static int frag_dwords(int cb, unsigned flags) { return (cb < 2 && (flags & EXL3_GEMV_FAST)) ? 16 : 8; }
 
-// k-tiles per split: aim for about 3-4 workgroups per CU (768-1024 in flight), each wavefront streaming at
-// least 4 iterations, and keep the staged activations within 40 KiB of LDS.
-static int auto_kt_per_split(int KT, int blocks, int rows, int frag_dw) {
+constexpr size_t kStageBudget = 48 * 1024;   // LDS bytes for the staged activations of one split
+
+static int max_kt_per_split(int frag_dw) { return (int)(kStageBudget / ((size_t)kMaxRows * frag_dw * 4)) / 4 * 4; }
+
+// k-tiles per split: aim for about 4 workgroups per CU (1024 in flight), each wavefront streaming at least
+// 4 iterations. The split depends only on the shape and the activation layout, never on the row count, so
+// every row is summed in the same order whatever the batch (row-exact results); the staged activations of
+// a split therefore fit the LDS budget at the maximum row count.
+static int auto_kt_per_split(int KT, int blocks, int frag_dw) {
   const int target_wgs = 1024;
   long want = ((long)KT * blocks + target_wgs - 1) / target_wgs;
   int kps = (int)((want + 3) / 4) * 4;
   if (kps < 16) kps = 16;
-  const int lds_cap = (40 * 1024) / (rows * frag_dw * 4);
-  int cap = (lds_cap / 4) * 4;
-  if (cap < 4) cap = 4;
+  const int cap = max_kt_per_split(frag_dw);
   if (kps > cap) kps = cap;
   const int ktr = ((KT + 3) / 4) * 4;
   if (kps > ktr) kps = ktr;
@@ -346,7 +360,7 @@ extern "C" size_t exl3_gemv_workspace_bytes(int k, int n_total, int rows, int K)
   if (k <= 0 || k % 16 || n_total <= 0 || n_total % 128 || rows < 1 || rows > kMaxRows || K < 1 || K > 8) return 0;
   const int KT = k / 16, blocks = n_total / 128;
   // the largest of the two activation layouts' splits
-  const int kps16 = auto_kt_per_split(KT, blocks, rows, 16), kps8 = auto_kt_per_split(KT, blocks, rows, 8);
+  const int kps16 = auto_kt_per_split(KT, blocks, 16), kps8 = auto_kt_per_split(KT, blocks, 8);
   const size_t a = workspace_for(KT, blocks, rows, n_total, kps16), b = workspace_for(KT, blocks, rows, n_total, kps8);
   return a > b ? a : b;
 }
@@ -384,8 +398,8 @@ extern "C" int exl3_gemv_ex(const uint16_t* xh, const uint32_t* const* trellis, 
   }
   const int KT = k / 16, blocks = n_total / 128;
   const int fd = frag_dwords(cb, flags);
-  int kps = kt_per_split > 0 ? ((kt_per_split + 3) / 4) * 4 : auto_kt_per_split(KT, blocks, rows, fd);
-  EXL3_REQUIRE((size_t)(kps + 4) * rows * fd * 4 <= 60 * 1024, EXL3_ERR_ARG,
+  int kps = kt_per_split > 0 ? ((kt_per_split + 3) / 4) * 4 : auto_kt_per_split(KT, blocks, fd);
+  EXL3_REQUIRE(((size_t)kps * rows + 1) * fd * 4 <= 60 * 1024, EXL3_ERR_ARG,
                "exl3_gemv: kt_per_split %d too large for %d rows", kps, rows);
   const int S = (KT + kps - 1) / kps;
   const size_t need = workspace_for(KT, blocks, rows, n_total, kps);
