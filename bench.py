@@ -1,0 +1,285 @@
+#!/usr/bin/env python3
+# SPDX-License-Identifier: Apache-2.0
+"""Fused EXL3 decode GEMV throughput on one MI355X (BASELINE.json metric, config 2).
+
+A step is one decode-layer pass of the EXL3 hot path at batch 1 on a 27B-class layer at K = 6 (6.0 bpw,
+3INST codebook), as the reference's fused decode path launches it (sibling groups, kernels.py:263-299,
+linear.py:124-193): q/k/v (5120 -> 6144 + 1024 + 1024, one launch), o (6144 -> 5120), gate/up
+(5120 -> 17408 + 17408, one launch), down (17408 -> 5120). Steps rotate over `--layers` distinct layers
+(default 6 = 1.53 GB of trellis) so the weights stream from HBM, not from the 256 MB Infinity Cache.
+Inputs (rotated activations, trellis, svh) are resident in HBM before timing starts.
+
+  value          whole-job GB/s: algorithmic bytes of all timed steps / wall time of the timed region
+                 (the steps replayed from one captured HIP graph, so host launch cost is excluded)
+  roofline       the GEMV kernel: algorithmic bytes per launch / its average launch duration, measured with
+                 HIP events on the launch stream, against the 8 TB/s HBM3E peak; traffic = HBM bytes per
+                 launch from rocprofv3 FETCH_SIZE / WRITE_SIZE (profiles/), or null
+  cpu_baseline   the NumPy oracle (reconstruct + fp32 matmul + Hadamard + svh) on the q projection
+
+    python bench.py [--gpus 1] [--steps 240] [--warmup 24] [--mode exact|fast]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+HBM_PEAK_GBS = 8000.0
+METRIC = "fused EXL3 GEMV GB/s (% HBM peak) at 6 bpw; 27B-shape decode tok/s"
+
+# (name, k, member output features)
+LAYER = [("qkv", 5120, [6144, 1024, 1024]), ("o", 6144, [5120]), ("gate_up", 5120, [17408, 17408]),
+         ("down", 17408, [5120])]
+
+
+def _import_package():
+    import importlib.util
+    name = "omlx_exl3_amd"
+    if name in sys.modules:
+        return sys.modules[name]
+    pkg_dir = os.path.join(ROOT, "omlx-exl3_amd")
+    spec = importlib.util.spec_from_file_location(name, os.path.join(pkg_dir, "__init__.py"),
+                                                  submodule_search_locations=[pkg_dir])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules[name] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def algorithmic_bytes(k: int, ns: list[int], K: int, rows: int) -> int:
+    """trellis + svh + rotated inputs (one per member) + output, per launch."""
+    n = sum(ns)
+    return sum(K * k * m // 8 for m in ns) + 2 * n + 2 * rows * k * len(ns) + 2 * rows * n
+
+
+def read_traffic(path: str):
+    """HBM bytes per GEMV launch from a committed rocprofv3 summary (lines 'key: value')."""
+    if not os.path.exists(path):
+        return None
+    vals = {}
+    for line in open(path):
+        if ":" in line and not line.lstrip().startswith("#"):
+            key, v = line.split(":", 1)
+            vals[key.strip()] = v.strip()
+    try:
+        return float(vals["hbm_bytes_per_launch"])
+    except (KeyError, ValueError):
+        return None
+
+
+def cpu_baseline(seconds_budget: float = 30.0) -> dict:
+    """NumPy oracle on the q projection (5120 -> 6144, K = 6): bit-exact reconstruct, rotation,
+    fp32 matmul, output Hadamard * svh. Median of 3 runs after one warm-up."""
+    import numpy as np
+
+    if ROOT not in sys.path:
+        sys.path.insert(0, ROOT)
+    from oracle import exl3_oracle as O
+
+    k, n, K = 5120, 6144, 6
+    rng = np.random.default_rng(7)
+    tr = O.random_trellis(k, n, K, 7)
+    su = np.where(rng.integers(0, 2, k) == 1, 1.0, -1.0).astype(np.float16)
+    sv = np.where(rng.integers(0, 2, n) == 1, 1.0, -1.0).astype(np.float16)
+    x = rng.standard_normal((1, k)).astype(np.float16)
+
+    def run():
+        t0 = time.perf_counter()
+        w = O.reconstruct_inner(tr, k, n, K, 0).view(np.float16).astype(np.float32)
+        t1 = time.perf_counter()
+        xh = O.rot(x, su.reshape(1, k))[0].astype(np.float32)
+        y = O.fwht128_f32(xh @ w) * O.HAD_SCALE * sv.astype(np.float32)
+        t2 = time.perf_counter()
+        return t1 - t0, t2 - t1, y
+
+    t_start = time.perf_counter()
+    run()
+    recs, mats = [], []
+    for _ in range(3):
+        a, b, _y = run()
+        recs.append(a)
+        mats.append(b)
+        if time.perf_counter() - t_start > seconds_budget:
+            break
+    rec, mat = statistics.median(recs), statistics.median(mats)
+    trellis_bytes = K * k * n // 8
+    cpu_model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    cores = len(os.sched_getaffinity(0))
+    return {
+        "value": round(trellis_bytes / (rec + mat) / 1e9, 5), "unit": "GB/s", "cores": cores, "kind": "port",
+        "sample": (f"q projection 5120->6144 K=6 (23.6 MB trellis), median of {len(recs)} runs: NumPy oracle "
+                   f"reconstruct {rec:.2f} s (single-threaded NumPy) + rotation/fp32 matmul/Hadamard {mat * 1e3:.1f} ms "
+                   f"(BLAS on {cores} visible cores); {cpu_model}"),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=240)
+    ap.add_argument("--warmup", type=int, default=24)
+    ap.add_argument("--mode", choices=["exact", "fast"], default="exact")
+    ap.add_argument("--layers", type=int, default=6, help="distinct layers in the rotating working set")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--traffic-file", default=os.path.join(ROOT, "profiles", "gemv_27b_k6_traffic.txt"))
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="run only a 1 GiB device copy (calibrates rocprofv3 FETCH/WRITE counters)")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one MI355X: this build has no multi-GPU path (the EXL3 linear would shard "
+              "column-/row-parallel over RCCL, see DESIGN.md); run with --gpus 1", file=sys.stderr)
+        return 2
+
+    import torch
+
+    dev = torch.device("cuda:0")
+    if args.copy_probe:
+        a = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+        b = torch.empty_like(a)
+        a.fill_(1)
+        for _ in range(5):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(10):
+            b.copy_(a)
+        e.record()
+        torch.cuda.synchronize()
+        ms = s.elapsed_time(e) / 10
+        print(json.dumps({"copy_bytes": 1 << 30, "copy_ms": ms, "copy_GBps_read_plus_write": 2 * (1 << 30) / ms / 1e6}))
+        return 0
+
+    pk = _import_package()
+    K, cb, rows = 6, 0, 1
+    fast = args.mode == "fast"
+    g = torch.Generator(device=dev).manual_seed(1234)
+    layers = []
+    for _ in range(args.layers):
+        items = []
+        for name, k, ns in LAYER:
+            trs = [torch.randint(-32768, 32768, (k // 16, n // 16, 16 * K), dtype=torch.int16, device=dev, generator=g)
+                   for n in ns]
+            svh = torch.where(torch.rand(sum(ns), device=dev, generator=g) < 0.5, -1.0, 1.0).half()
+            xh = torch.randn((len(ns), rows, k), device=dev, generator=g).half()
+            plan = pk.kernels.TrellisGemvPlan(k, ns, K, cb, svh, rows, torch.float16, fast=fast)
+            out = torch.empty((rows, sum(ns)), dtype=torch.float16, device=dev)
+            items.append((name, plan, xh, trs, out, algorithmic_bytes(k, ns, K, rows)))
+        layers.append(items)
+    step_bytes = sum(it[5] for it in layers[0])
+    L = args.layers
+
+    def run_layer(items):
+        for _name, plan, xh, trs, out, _b in items:
+            plan(xh, trs, out=out)
+
+    # warm-up (eager)
+    for i in range(args.warmup):
+        run_layer(layers[i % L])
+    torch.cuda.synchronize()
+
+    # ---- per-launch kernel durations (HIP events on the launch stream) ----
+    n_evt = max(L, (args.steps // L) * L)
+    per = {name: [] for name, _, _ in LAYER}
+    evs = []
+    for i in range(n_evt):
+        for name, plan, xh, trs, out, nbytes in layers[i % L]:
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record()
+            plan(xh, trs, out=out)
+            e.record()
+            evs.append((name, nbytes, s, e))
+    torch.cuda.synchronize()
+    tot_bytes = tot_ms = 0.0
+    for name, nbytes, s, e in evs:
+        ms = s.elapsed_time(e)
+        per[name].append((nbytes, ms))
+        tot_bytes += nbytes
+        tot_ms += ms
+    kernel_gbs = tot_bytes / tot_ms / 1e6
+    per_shape = {}
+    for name, rec in per.items():
+        nb = rec[0][0]
+        med = statistics.median(ms for _, ms in rec)
+        per_shape[name] = {"bytes": nb, "median_us": round(med * 1e3, 2), "GB_s": round(nb / med / 1e6, 1),
+                           "pct_hbm_peak": round(100 * nb / med / 1e6 / HBM_PEAK_GBS, 1)}
+
+    # ---- whole-job throughput: all layers captured in one graph, replayed ----
+    reps = max(1, args.steps // L)
+    graph = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream(device=dev)
+    cap.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(cap):
+        for items in layers:           # one eager pass on the capture stream before capture
+            run_layer(items)
+    torch.cuda.current_stream(dev).wait_stream(cap)
+    torch.cuda.synchronize()
+    ref_out = [it[4].clone() for it in layers[-1]]
+    with torch.cuda.graph(graph):
+        for items in layers:
+            run_layer(items)
+    graph.replay()
+    torch.cuda.synchronize()
+    for it, r in zip(layers[-1], ref_out):
+        if not torch.equal(it[4], r):
+            print("graph replay differs from the eager result", file=sys.stderr)
+            return 1
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        graph.replay()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    steps = reps * L
+    value = step_bytes * steps / wall / 1e9
+
+    traffic = read_traffic(args.traffic_file)
+    per_launch_bytes = tot_bytes / len(evs)
+    avg_launch_ms = tot_ms / len(evs)
+    result = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall / steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic",
+        "config": {"workload": ("27B-class decode layer, batch 1, K=6 (6.0 bpw) 3INST: fused GEMV launches qkv "
+                                "5120->6144+1024+1024, o 6144->5120, gate_up 5120->17408+17408, down 17408->5120; "
+                                f"{L} distinct layers rotated ({step_bytes * L / 1e9:.2f} GB of weights)"),
+                   "global_batch": rows, "bpw": K, "codebook": "3inst", "gemv_mode": args.mode,
+                   "parallelism": "none (1 GPU)"},
+        "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 1),
+        "roofline": {"bound": "hbm", "achieved": round(kernel_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(kernel_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": traffic,
+                     "algorithmic_bytes_per_launch": round(per_launch_bytes),
+                     "avg_launch_us": round(avg_launch_ms * 1e3, 3)},
+        "per_shape": per_shape,
+        "decode_tok_s": None,
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(result))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

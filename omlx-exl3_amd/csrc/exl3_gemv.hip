@@ -37,6 +37,7 @@ struct GemvArgs {
   void* y;
   float* partials;
   uint32_t* counters;
+  const uint16_t* xzero;
   int k, KT, rows, n_total, S, kt_per_split;
 };
 
@@ -108,12 +109,32 @@ __device__ __forceinline__ u32x4 mfma_src(uint32_t a, uint32_t b, uint32_t c, ui
   return u32x4{a, b, c, d};
 }
 
+// One prefetch set of a lane: its run's K stream words, the word before the run and (pair layout) the
+// 16 activations of its k-tile for its batch row, loaded straight from xh (L2-resident, no staging).
+template <int K, bool GA>
+struct Stage {
+  uint32_t w[K];
+  uint32_t wp;
+  u32x4 x0, x1;
+};
+
+template <int K, bool GA>
+__device__ __forceinline__ void issue(Stage<K, GA>& st, const uint32_t* __restrict__ tp, int g,
+                                      const uint16_t* __restrict__ xp) {
+  load_run<K>(tp, g, st.w, st.wp);
+  if constexpr (GA) {
+    st.x0 = reinterpret_cast<const u32x4*>(xp)[0];
+    st.x1 = reinterpret_cast<const u32x4*>(xp)[1];
+  }
+}
+
 template <int K, int CB, bool FAST, int OT>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   constexpr bool SPLIT = FAST && CB < 2;
-  constexpr int FRAG_DW = SPLIT ? 16 : 8;     // staged activation dwords per (k-tile, row)
+  constexpr bool GA = !SPLIT;                  // activations from global memory (pair layout)
+  constexpr int FRAG_DW = 16;                  // staged activation dwords per (k-tile, row), split layout
   constexpr int TW = 8 * K;
-  extern __shared__ uint32_t xs[];            // [nkt_pad][rows][FRAG_DW] + one zero record
+  extern __shared__ uint32_t xs[];             // split layout: [iters*4][rows][16] + one zero record
   __shared__ float bv[kMaxRows][128];
   __shared__ uint32_t last;
 
@@ -131,50 +152,55 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   const int iters = (nkt + 3) >> 2;
   const int nrec = iters * 4 * rows;
 
-  // ---- stage this k-range of the activations in the MFMA A-operand order ----
-  for (int idx = tid; idx < (nrec + 1) * FRAG_DW; idx += 256) {
-    const int rec = idx / FRAG_DW, d = idx % FRAG_DW;
-    uint32_t v = 0;
-    if (rec < nrec) {
-      const int kl = rec / rows, r = rec % rows;
-      if (kl < nkt) {
-        const size_t base = (size_t)r * a.k + (size_t)(kt0 + kl) * 16;
-        if constexpr (SPLIT) {
+  if constexpr (SPLIT) {
+    // stage this k-range of the activations, each value twice (the A operand of a split B register)
+    for (int idx = tid; idx < (nrec + 1) * FRAG_DW; idx += 256) {
+      const int rec = idx / FRAG_DW, d = idx % FRAG_DW;
+      uint32_t v = 0;
+      if (rec < nrec) {
+        const int kl = rec / rows, r = rec % rows;
+        if (kl < nkt) {
           const int j = d >> 2, e = d & 3;
-          const uint32_t x = xh[base + 2 * j + (e & 1) + 8 * (e >> 1)];
+          const uint32_t x = xh[(size_t)r * a.k + (size_t)(kt0 + kl) * 16 + 2 * j + (e & 1) + 8 * (e >> 1)];
           v = x | (x << 16);
-        } else {
-          const int jj = d >> 2, e = d & 3;
-          const int di = ((e & 1) ? 4 : 0) + (e >> 1) + 2 * jj;   // {0,4,1,5}[e] + 2jj
-          v = reinterpret_cast<const uint32_t*>(xh + base)[di];
         }
       }
+      xs[idx] = v;
     }
-    xs[idx] = v;
+    __syncthreads();
   }
-  __syncthreads();
 
   const int q = lane >> 4, c = lane & 15, g = c & 7;
   const int nt_local = (blk - blk0) * 8 + wave * 2 + (c >> 3);
   const uint32_t* __restrict__ tbase = tr + (size_t)nt_local * TW;
   const size_t kstride = (size_t)NT * TW;
-  // A operand: row c of the batch, k-group q; rows >= `rows` read the zero record
-  const bool active = c < rows;
+  const uint32_t* __restrict__ tlast = tbase + (size_t)(kt1 - 1) * kstride;
+  const bool active = c < rows;                // this lane's A-operand batch row exists
+  // split layout: rows >= `rows` read the zero record of the staging buffer
   const uint32_t* xa = xs + (active ? (size_t)(q * rows + c) * FRAG_DW : (size_t)nrec * FRAG_DW);
   const int xa_step = active ? 4 * rows * FRAG_DW : 0;
+  // pair layout: A straight from xh; absent rows and k-tiles past the split read a zeroed 64-byte region
+  const uint16_t* __restrict__ xzero = a.xzero;
   const uint32_t xor_v = kXor3;
 
   f32x4 acc_lo = {0.f, 0.f, 0.f, 0.f}, acc_hi = {0.f, 0.f, 0.f, 0.f};
 
-  auto kt_of = [&](int it) { return min(kt0 + 4 * it + q, kt1 - 1); };
-  auto process = [&](const uint32_t* w, uint32_t wp, const uint32_t* xrec) {
+  auto issue_it = [&](Stage<K, GA>& st, int it) {
+    const int kt = kt0 + 4 * it + q;
+    const bool ok = kt < kt1;
+    const uint32_t* tp = ok ? tbase + (size_t)kt * kstride : tlast;
+    const uint16_t* xp = (ok && active) ? xh + (size_t)c * a.k + (size_t)kt * 16 : xzero;
+    issue<K, GA>(st, tp, g, xp);
+  };
+
+  auto process = [&](const Stage<K, GA>& st, int it) {
     if constexpr (SPLIT) {
       uint32_t b[32];
-      decode_run<K, CB, true>(w, wp, b, xor_v);
+      decode_run<K, CB, true>(st.w, st.wp, b, xor_v);
+      const uint32_t* xrec = xa + (size_t)it * xa_step;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const u32x4 av = reinterpret_cast<const u32x4*>(xrec)[j];
-        const f16x8 A = as_f16x8(av);
+        const f16x8 A = as_f16x8(reinterpret_cast<const u32x4*>(xrec)[j]);
         acc_lo = __builtin_amdgcn_mfma_f32_16x16x32_f16(
             A, as_f16x8(mfma_src(b[8 * j], b[8 * j + 1], b[8 * j + 2], b[8 * j + 3])), acc_lo, 0, 0, 0);
         acc_hi = __builtin_amdgcn_mfma_f32_16x16x32_f16(
@@ -182,38 +208,37 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
       }
     } else {
       uint32_t b[16];
-      decode_run<K, CB, false>(w, wp, b, xor_v);
-#pragma unroll
-      for (int jj = 0; jj < 2; ++jj) {
-        const f16x8 A = as_f16x8(reinterpret_cast<const u32x4*>(xrec)[jj]);
-        // positions 16jj + 4half + {0..3} and 16jj + 8 + 4half + {0..3}: registers (8jj + 2half + {0,1}),
-        // (8jj + 4 + 2half + {0,1})
-        acc_lo = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-            A, as_f16x8(mfma_src(b[8 * jj], b[8 * jj + 1], b[8 * jj + 4], b[8 * jj + 5])), acc_lo, 0, 0, 0);
-        acc_hi = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-            A, as_f16x8(mfma_src(b[8 * jj + 2], b[8 * jj + 3], b[8 * jj + 6], b[8 * jj + 7])), acc_hi, 0, 0, 0);
-      }
+      decode_run<K, CB, false>(st.w, st.wp, b, xor_v);
+      // A fragments: k pairs (0,1) (8,9) (2,3) (10,11) and (4,5) (12,13) (6,7) (14,15) of the k-tile
+      const f16x8 A0 = as_f16x8(u32x4{st.x0.x, st.x1.x, st.x0.y, st.x1.y});
+      const f16x8 A1 = as_f16x8(u32x4{st.x0.z, st.x1.z, st.x0.w, st.x1.w});
+      // positions 16jj + 4half + {0..3} and 16jj + 8 + 4half + {0..3}: registers (8jj + 2half + {0,1}),
+      // (8jj + 4 + 2half + {0,1})
+      acc_lo = __builtin_amdgcn_mfma_f32_16x16x32_f16(A0, as_f16x8(mfma_src(b[0], b[1], b[4], b[5])), acc_lo, 0, 0, 0);
+      acc_hi = __builtin_amdgcn_mfma_f32_16x16x32_f16(A0, as_f16x8(mfma_src(b[2], b[3], b[6], b[7])), acc_hi, 0, 0, 0);
+      acc_lo = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1, as_f16x8(mfma_src(b[8], b[9], b[12], b[13])), acc_lo, 0, 0, 0);
+      acc_hi = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1, as_f16x8(mfma_src(b[10], b[11], b[14], b[15])), acc_hi, 0, 0,
+                                                      0);
     }
   };
 
-  uint32_t wa[K], wb[K], wc[K];
-  uint32_t pa, pb, pc;
-  load_run<K>(tbase + kt_of(0) * kstride, g, wa, pa);
-  load_run<K>(tbase + kt_of(1) * kstride, g, wb, pb);
-  int it = 0;
-  for (; it + 1 < iters; it += 2) {
-#pragma unroll
-    for (int i = 0; i < K; ++i) wc[i] = wa[i];
-    pc = pa;
-    load_run<K>(tbase + kt_of(it + 2) * kstride, g, wa, pa);
-    process(wc, pc, xa + (size_t)it * xa_step);
-#pragma unroll
-    for (int i = 0; i < K; ++i) wc[i] = wb[i];
-    pc = pb;
-    load_run<K>(tbase + kt_of(it + 3) * kstride, g, wb, pb);
-    process(wc, pc, xa + (size_t)(it + 1) * xa_step);
+  // Three prefetch sets rotate without copies, so each wait is for exactly the set about to be used while
+  // the two younger sets stay in flight. Prefetches past the split re-read its last tile (clamped).
+  Stage<K, GA> sa, sb, sc;
+  issue_it(sa, 0);
+  issue_it(sb, 1);
+  issue_it(sc, 2);
+  for (int it = 0;;) {
+    process(sa, it);
+    issue_it(sa, it + 3);
+    if (++it >= iters) break;
+    process(sb, it);
+    issue_it(sb, it + 3);
+    if (++it >= iters) break;
+    process(sc, it);
+    issue_it(sc, it + 3);
+    if (++it >= iters) break;
   }
-  if (it < iters) process(wa, pa, xa + (size_t)it * xa_step);
 
   // ---- columns of this wavefront -> block partial (LDS) ----
   const int col_lo = (wave * 2 + (c >> 3)) * 16 + g, col_hi = col_lo + 8;
@@ -228,14 +253,20 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   __syncthreads();
 
   // ---- k-splits across workgroups: the last arriver sums the partials in split order ----
+  // Cross-workgroup traffic uses device-scope relaxed atomic stores and loads, which the hardware performs at
+  // the device coherence point (through the per-XCD L2s), so no cache-wide write-back or invalidate is needed:
+  // each thread waits until its own stores are acknowledged before the workgroup bumps the block's counter,
+  // and the last arriver reads the partials back with device-scope loads.
   if (a.S > 1) {
     float* part = a.partials;
     const size_t pstride = (size_t)rows * a.n_total;
     for (int idx = tid; idx < rows * 128; idx += 256) {
       const int r = idx >> 7, cc = idx & 127;
-      part[(size_t)s * pstride + (size_t)r * a.n_total + blk * 128 + cc] = bv[r][cc];
+      __hip_atomic_store(part + (size_t)s * pstride + (size_t)r * a.n_total + blk * 128 + cc, bv[r][cc],
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    // this thread's device-scope stores are acknowledged (vmcnt counts stores on gfx9) before the barrier
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (tid == 0) {
       const uint32_t prev = __hip_atomic_fetch_add(&a.counters[blk], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -243,12 +274,12 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     }
     __syncthreads();
     if (last == 0) return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     for (int idx = tid; idx < rows * 128; idx += 256) {
       const int r = idx >> 7, cc = idx & 127;
       const float* src = part + (size_t)r * a.n_total + blk * 128 + cc;
       float v = 0.f;
-      for (int ss = 0; ss < a.S; ++ss) v += __builtin_nontemporal_load(src + (size_t)ss * pstride);
+      for (int ss = 0; ss < a.S; ++ss)
+        v += __hip_atomic_load(src + (size_t)ss * pstride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       bv[r][cc] = v;
     }
     if (tid == 0) __hip_atomic_store(&a.counters[blk], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -292,32 +323,33 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
 // ------------------------------------------------------------------------------------------------
 // host side
 // ------------------------------------------------------------------------------------------------
-static int frag_dwords(int cb, unsigned flags) { return (cb < 2 && (flags & EXL3_GEMV_FAST)) ? 16 : 8; }
+static bool split_layout(int cb, unsigned flags) { return cb < 2 && (flags & EXL3_GEMV_FAST); }
 
-constexpr size_t kStageBudget = 48 * 1024;   // LDS bytes for the staged activations of one split
+constexpr int kResidentWgs = 1024;           // 256 CUs x 4 workgroups of 4 wavefronts (VGPR-limited occupancy)
+constexpr size_t kStageBudget = 48 * 1024;   // LDS bytes for the staged activations of one split (split layout)
 
-static int max_kt_per_split(int frag_dw) { return (int)(kStageBudget / ((size_t)kMaxRows * frag_dw * 4)) / 4 * 4; }
-
-// k-tiles per split: aim for about 4 workgroups per CU (1024 in flight), each wavefront streaming at least
-// 4 iterations. The split depends only on the shape and the activation layout, never on the row count, so
-// every row is summed in the same order whatever the batch (row-exact results); the staged activations of
-// a split therefore fit the LDS budget at the maximum row count.
-static int auto_kt_per_split(int KT, int blocks, int frag_dw) {
-  const int target_wgs = 1024;
-  long want = ((long)KT * blocks + target_wgs - 1) / target_wgs;
-  int kps = (int)((want + 3) / 4) * 4;
-  if (kps < 16) kps = 16;
-  const int cap = max_kt_per_split(frag_dw);
-  if (kps > cap) kps = cap;
-  const int ktr = ((KT + 3) / 4) * 4;
-  if (kps > ktr) kps = ktr;
-  return kps;
+// k-tiles per split. The grid (blocks x S workgroups) is sized to one resident round of workgroups, so no
+// workgroup waits for a second round, with splits as long as that allows (fewer partial sums, longer
+// streams per wavefront). The split depends only on the shape and the activation layout, never on the row
+// count, so each row is summed in the same order whatever the batch (row-exact results). The split
+// layout stages its activations in LDS, which caps its split at the maximum row count.
+static int auto_kt_per_split(int KT, int blocks, bool split) {
+  const int S_occ = blocks >= kResidentWgs ? 1 : kResidentWgs / blocks;
+  int kps = (KT + S_occ - 1) / S_occ;
+  kps = (kps + 3) / 4 * 4;
+  if (split) {
+    const int cap = (int)(kStageBudget / ((size_t)kMaxRows * 16 * 4)) / 4 * 4;
+    if (kps > cap) kps = cap;
+  }
+  return kps < 4 ? 4 : kps;
 }
+
+// workspace: [per-block counters, padded to 256 B][256 zero bytes][S x rows x n_total fp32 partials]
+static size_t counters_bytes(int blocks) { return ((size_t)blocks * sizeof(uint32_t) + 255) / 256 * 256; }
 
 static size_t workspace_for(int KT, int blocks, int rows, int n_total, int kps) {
   const int S = (KT + kps - 1) / kps;
-  size_t bytes = (size_t)blocks * sizeof(uint32_t);
-  bytes = (bytes + 255) / 256 * 256;
+  size_t bytes = counters_bytes(blocks) + 256;
   if (S > 1) bytes += (size_t)S * rows * n_total * sizeof(float);
   return bytes;
 }
@@ -360,8 +392,8 @@ extern "C" size_t exl3_gemv_workspace_bytes(int k, int n_total, int rows, int K)
   if (k <= 0 || k % 16 || n_total <= 0 || n_total % 128 || rows < 1 || rows > kMaxRows || K < 1 || K > 8) return 0;
   const int KT = k / 16, blocks = n_total / 128;
   // the largest of the two activation layouts' splits
-  const int kps16 = auto_kt_per_split(KT, blocks, 16), kps8 = auto_kt_per_split(KT, blocks, 8);
-  const size_t a = workspace_for(KT, blocks, rows, n_total, kps16), b = workspace_for(KT, blocks, rows, n_total, kps8);
+  const int kps_s = auto_kt_per_split(KT, blocks, true), kps_p = auto_kt_per_split(KT, blocks, false);
+  const size_t a = workspace_for(KT, blocks, rows, n_total, kps_s), b = workspace_for(KT, blocks, rows, n_total, kps_p);
   return a > b ? a : b;
 }
 
@@ -397,22 +429,22 @@ extern "C" int exl3_gemv_ex(const uint16_t* xh, const uint32_t* const* trellis, 
     a.blk_end[i] = 1 << 30;
   }
   const int KT = k / 16, blocks = n_total / 128;
-  const int fd = frag_dwords(cb, flags);
-  int kps = kt_per_split > 0 ? ((kt_per_split + 3) / 4) * 4 : auto_kt_per_split(KT, blocks, fd);
-  EXL3_REQUIRE(((size_t)kps * rows + 1) * fd * 4 <= 60 * 1024, EXL3_ERR_ARG,
+  const bool split = split_layout(cb, flags);
+  int kps = kt_per_split > 0 ? ((kt_per_split + 3) / 4) * 4 : auto_kt_per_split(KT, blocks, split);
+  EXL3_REQUIRE(!split || ((size_t)kps * rows + 1) * 16 * 4 <= 60 * 1024, EXL3_ERR_ARG,
                "exl3_gemv: kt_per_split %d too large for %d rows", kps, rows);
   const int S = (KT + kps - 1) / kps;
   const size_t need = workspace_for(KT, blocks, rows, n_total, kps);
-  EXL3_REQUIRE(S == 1 || (workspace && workspace_bytes >= need), EXL3_ERR_WORKSPACE,
-               "exl3_gemv: workspace of %zu bytes needed (got %zu)", need, workspace_bytes);
+  EXL3_REQUIRE(workspace && workspace_bytes >= need && aligned(workspace, 256), EXL3_ERR_WORKSPACE,
+               "exl3_gemv: a zero-initialised, 256-byte aligned workspace of %zu bytes is needed (got %zu)", need,
+               workspace_bytes);
   a.xh = xh;
   a.svh = svh;
   a.bias = bias;
   a.y = y;
   a.counters = static_cast<uint32_t*>(workspace);
-  a.partials = workspace ? reinterpret_cast<float*>(static_cast<char*>(workspace) +
-                                                    ((size_t)blocks * sizeof(uint32_t) + 255) / 256 * 256)
-                         : nullptr;
+  a.xzero = reinterpret_cast<const uint16_t*>(static_cast<char*>(workspace) + counters_bytes(blocks));
+  a.partials = reinterpret_cast<float*>(static_cast<char*>(workspace) + counters_bytes(blocks) + 256);
   a.k = k;
   a.KT = KT;
   a.rows = rows;
@@ -420,7 +452,7 @@ extern "C" int exl3_gemv_ex(const uint16_t* xh, const uint32_t* const* trellis, 
   a.S = S;
   a.kt_per_split = kps;
   const int iters_max = (kps + 3) / 4;
-  const size_t smem = ((size_t)iters_max * 4 * rows + 1) * fd * 4;
+  const size_t smem = split ? ((size_t)iters_max * 4 * rows + 1) * 16 * 4 : 0;
   const bool fast = (flags & EXL3_GEMV_FAST) != 0;
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (K) {
