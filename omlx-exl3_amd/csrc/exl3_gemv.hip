@@ -37,11 +37,11 @@ struct GemvArgs {
   void* y;
   float* partials;
   uint32_t* counters;
-  const uint16_t* xzero;
   int k, KT, rows, n_total, S, kt_per_split;
 };
 
 constexpr int kMaxRows = 16;
+constexpr int kBufferFlags = 0x00020000;   // raw buffer descriptor word 3 (32-bit data, no swizzle) for gfx950
 
 __device__ __forceinline__ uint32_t bitop_split(uint32_t h, uint32_t mask_s, uint32_t xor_v) {
   uint32_t u;
@@ -73,27 +73,28 @@ __device__ __forceinline__ void decode_run(const uint32_t* w, uint32_t wp, uint3
   }
 }
 
+// Buffer loads of a run's K stream words (at byte offset vo) and the word before the run (at vo_wp), both
+// advanced by the wave-uniform soff. The workgroup's buffer descriptor ends at the end of its k-split, so
+// prefetches past the split return zeros without touching memory.
 template <int K>
-__device__ __forceinline__ void load_run(const uint32_t* __restrict__ tp, int g, uint32_t* w, uint32_t& wp) {
-  constexpr int TW = 8 * K;
-  const uint32_t* p = tp + K * g;
-  if constexpr (K % 4 == 0) {
+__device__ __forceinline__ void load_run(__amdgpu_buffer_rsrc_t rs, uint32_t vo, uint32_t vo_wp, uint32_t soff,
+                                         uint32_t* w, uint32_t& wp) {
+  int i = 0;
 #pragma unroll
-    for (int i = 0; i < K / 4; ++i) {
-      const u32x4 v = reinterpret_cast<const u32x4*>(p)[i];
-      w[4 * i] = v.x; w[4 * i + 1] = v.y; w[4 * i + 2] = v.z; w[4 * i + 3] = v.w;
-    }
-  } else if constexpr (K % 2 == 0) {
-#pragma unroll
-    for (int i = 0; i < K / 2; ++i) {
-      const u32x2 v = reinterpret_cast<const u32x2*>(p)[i];
-      w[2 * i] = v.x; w[2 * i + 1] = v.y;
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < K; ++i) w[i] = p[i];
+  for (; i + 4 <= K; i += 4) {
+    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, vo + 4 * i, soff, 0);
+    w[i] = v.x; w[i + 1] = v.y; w[i + 2] = v.z; w[i + 3] = v.w;
   }
-  wp = tp[(K * g + TW - 1) % TW];
+  if constexpr (K % 4 == 3) {
+    const u32x3 v = __builtin_amdgcn_raw_buffer_load_b96(rs, vo + 4 * (K - 3), soff, 0);
+    w[K - 3] = v.x; w[K - 2] = v.y; w[K - 1] = v.z;
+  } else if constexpr (K % 4 == 2) {
+    const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rs, vo + 4 * (K - 2), soff, 0);
+    w[K - 2] = v.x; w[K - 1] = v.y;
+  } else if constexpr (K % 4 == 1) {
+    w[K - 1] = __builtin_amdgcn_raw_buffer_load_b32(rs, vo + 4 * (K - 1), soff, 0);
+  }
+  wp = __builtin_amdgcn_raw_buffer_load_b32(rs, vo_wp, soff, 0);
 }
 
 template <typename T>
@@ -109,32 +110,37 @@ __device__ __forceinline__ u32x4 mfma_src(uint32_t a, uint32_t b, uint32_t c, ui
   return u32x4{a, b, c, d};
 }
 
-// One prefetch set of a lane: its run's K stream words, the word before the run and (pair layout) the
-// 16 activations of its k-tile for its batch row, loaded straight from xh (L2-resident, no staging).
-template <int K, bool GA>
+// Activation (A operand) layouts of the kernel:
+//   kPair   B registers hold two fp16-rounded codebook values (k pair); A = xh's natural fp16 pairs
+//   kSplit  B registers hold the two fp16 summands of one value; A = each activation twice, built from the
+//           natural pairs with byte permutes (2 instructions per k pair)
+enum Layout : int { kPair = 0, kSplit = 1 };
+
+// One trellis prefetch set of a lane: its run's K stream words and the word before the run.
+template <int K>
 struct Stage {
   uint32_t w[K];
   uint32_t wp;
-  u32x4 x0, x1;
 };
 
-template <int K, bool GA>
-__device__ __forceinline__ void issue(Stage<K, GA>& st, const uint32_t* __restrict__ tp, int g,
-                                      const uint16_t* __restrict__ xp) {
-  load_run<K>(tp, g, st.w, st.wp);
-  if constexpr (GA) {
-    st.x0 = reinterpret_cast<const u32x4*>(xp)[0];
-    st.x1 = reinterpret_cast<const u32x4*>(xp)[1];
-  }
+__device__ __forceinline__ u32x4 dup4(uint32_t d0, uint32_t d1) {   // (x0,x1),(x2,x3) -> x0 x0, x1 x1, x2 x2, x3 x3
+  return u32x4{__builtin_amdgcn_perm(d0, d0, 0x01000100u), __builtin_amdgcn_perm(d0, d0, 0x03020302u),
+               __builtin_amdgcn_perm(d1, d1, 0x01000100u), __builtin_amdgcn_perm(d1, d1, 0x03020302u)};
 }
 
-template <int K, int CB, bool FAST, int OT>
+// Trellis sets in flight per lane. Decoding keeps the VALU busy for ~1 us per set per SIMD, so only the
+// sets queued behind the one being decoded hide memory latency; at full streaming rate the loaded latency
+// is several microseconds, which takes several sets per wavefront (an even number: the activation
+// registers alternate by phase parity).
+constexpr int kDepth = 4;
+
+template <int K, int CB, int L, int OT>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
-  constexpr bool SPLIT = FAST && CB < 2;
-  constexpr bool GA = !SPLIT;                  // activations from global memory (pair layout)
-  constexpr int FRAG_DW = 16;                  // staged activation dwords per (k-tile, row), split layout
+  constexpr bool SPLIT = L == kSplit;
   constexpr int TW = 8 * K;
-  extern __shared__ uint32_t xs[];             // split layout: [iters*4][rows][16] + one zero record
+  constexpr int D = kDepth;
+  static_assert(D % 2 == 0, "activation registers alternate by phase parity");
+  extern __shared__ u32x4 xs[];   // split's activations: [(iters+1)*4 k-tiles][rows] records of 32 B + zero record
   __shared__ float bv[kMaxRows][128];
   __shared__ uint32_t last;
 
@@ -145,100 +151,117 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   const uint32_t* __restrict__ tr = a.tr[m];
   const int NT = a.NT[m];
   const int rows = a.rows;
-  const uint16_t* __restrict__ xh = a.xh + (size_t)m * rows * a.k;
   const int kt0 = s * a.kt_per_split;
   const int kt1 = min(a.KT, kt0 + a.kt_per_split);
   const int nkt = kt1 - kt0;
   const int iters = (nkt + 3) >> 2;
-  const int nrec = iters * 4 * rows;
-
-  if constexpr (SPLIT) {
-    // stage this k-range of the activations, each value twice (the A operand of a split B register)
-    for (int idx = tid; idx < (nrec + 1) * FRAG_DW; idx += 256) {
-      const int rec = idx / FRAG_DW, d = idx % FRAG_DW;
-      uint32_t v = 0;
-      if (rec < nrec) {
-        const int kl = rec / rows, r = rec % rows;
-        if (kl < nkt) {
-          const int j = d >> 2, e = d & 3;
-          const uint32_t x = xh[(size_t)r * a.k + (size_t)(kt0 + kl) * 16 + 2 * j + (e & 1) + 8 * (e >> 1)];
-          v = x | (x << 16);
-        }
-      }
-      xs[idx] = v;
-    }
-    __syncthreads();
-  }
 
   const int q = lane >> 4, c = lane & 15, g = c & 7;
   const int nt_local = (blk - blk0) * 8 + wave * 2 + (c >> 3);
-  const uint32_t* __restrict__ tbase = tr + (size_t)nt_local * TW;
-  const size_t kstride = (size_t)NT * TW;
-  const uint32_t* __restrict__ tlast = tbase + (size_t)(kt1 - 1) * kstride;
-  const bool active = c < rows;                // this lane's A-operand batch row exists
-  // split layout: rows >= `rows` read the zero record of the staging buffer
-  const uint32_t* xa = xs + (active ? (size_t)(q * rows + c) * FRAG_DW : (size_t)nrec * FRAG_DW);
-  const int xa_step = active ? 4 * rows * FRAG_DW : 0;
-  // pair layout: A straight from xh; absent rows and k-tiles past the split read a zeroed 64-byte region
-  const uint16_t* __restrict__ xzero = a.xzero;
-  const uint32_t xor_v = kXor3;
+  const uint32_t kstride = (uint32_t)NT * TW;   // words per k-tile row of the member's trellis
+  // trellis of this split: k-tile rows [kt0, kt1); lane q of iteration it reads row kt0 + 4 it + q. The
+  // descriptor ends at the split's end: prefetches past it (and k-tiles past it) read zeros, no traffic.
+  const __amdgpu_buffer_rsrc_t rs_t = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint32_t*>(tr + (size_t)kt0 * kstride), (short)0, (int)((uint32_t)nkt * kstride * 4u), kBufferFlags);
+  const uint32_t vo_t = ((uint32_t)q * kstride + (uint32_t)nt_local * TW + K * g) * 4u;
+  const uint32_t vo_wp = ((uint32_t)q * kstride + (uint32_t)nt_local * TW + (K * g + TW - 1) % TW) * 4u;
+  const uint32_t step_t = 16u * kstride;          // bytes per iteration (4 k-tile rows)
 
-  f32x4 acc_lo = {0.f, 0.f, 0.f, 0.f}, acc_hi = {0.f, 0.f, 0.f, 0.f};
-
-  auto issue_it = [&](Stage<K, GA>& st, int it) {
-    const int kt = kt0 + 4 * it + q;
-    const bool ok = kt < kt1;
-    const uint32_t* tp = ok ? tbase + (size_t)kt * kstride : tlast;
-    const uint16_t* xp = (ok && active) ? xh + (size_t)c * a.k + (size_t)kt * 16 : xzero;
-    issue<K, GA>(st, tp, g, xp);
+  auto issue_it = [&](Stage<K>& st, int it) {
+    // the iteration index is wave-uniform: keep the advancing offset in an SGPR (buffer soffset)
+    load_run<K>(rs_t, vo_t, vo_wp, __builtin_amdgcn_readfirstlane((uint32_t)it * step_t), st.w, st.wp);
   };
 
-  auto process = [&](const Stage<K, GA>& st, int it) {
+  Stage<K> st[D];
+  static_for<0, D>([&](auto P) {
+    issue_it(st[decltype(P)::value], decltype(P)::value);
+    __builtin_amdgcn_sched_barrier(0);
+  });
+
+  // ---- stage this split's activations in LDS (natural layout), zero past the split ----
+  // record (kl, r) = the 16 activations of k-tile kt0 + kl for batch row r; one extra iteration of zero
+  // records (read by the last phase's look-ahead) and a zero record for absent rows at the end
+  const int nrec = (iters + 1) * 4 * rows;
+  {
+    const uint16_t* __restrict__ xh = a.xh + (size_t)m * rows * a.k;
+    for (int idx = tid; idx < (nrec + 1) * 2; idx += 256) {
+      const int rec = idx >> 1, h = idx & 1;
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (rec < nrec) {
+        const int kl = rec / rows, r = rec - kl * rows;
+        if (kl < nkt) v = reinterpret_cast<const u32x4*>(xh + (size_t)r * a.k + (size_t)(kt0 + kl) * 16)[h];
+      }
+      xs[idx] = v;
+    }
+  }
+  __syncthreads();
+
+  // A operand of lane (q, c): batch row c of k-tile kt0 + 4 it + q; absent rows read the zero record
+  const bool active = c < rows;
+  const u32x4* xa = xs + (active ? (size_t)(q * rows + c) * 2 : (size_t)nrec * 2);
+  const int xa_step = active ? 4 * rows * 2 : 0;
+  auto read_A = [&](int it, u32x4 (&A)[2]) {
+    const u32x4* p = xa + (size_t)it * xa_step;
+    A[0] = p[0];
+    A[1] = p[1];
+  };
+
+  const uint32_t xor_v = kXor3;
+  f32x4 acc_lo = {0.f, 0.f, 0.f, 0.f}, acc_hi = {0.f, 0.f, 0.f, 0.f};
+
+  auto mfma = [](f32x4& acc, u32x4 A, u32x4 B) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_f16x8(A), as_f16x8(B), acc, 0, 0, 0);
+  };
+
+  auto process = [&](const Stage<K>& st, const u32x4 (&X)[2]) {
     if constexpr (SPLIT) {
       uint32_t b[32];
       decode_run<K, CB, true>(st.w, st.wp, b, xor_v);
-      const uint32_t* xrec = xa + (size_t)it * xa_step;
+      // A_j = activations k = 4j..4j+3, each twice; B = the summand registers of those k:
+      // k 4j, 4j+1 are positions 16(j%2) + 2(j/2) + {0, 1}, k 4j+2, 4j+3 positions 16(j%2) + 8 + 2(j/2) + {0, 1}
+      const u32x4 A[4] = {dup4(X[0].x, X[0].y), dup4(X[0].z, X[0].w), dup4(X[1].x, X[1].y), dup4(X[1].z, X[1].w)};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const f16x8 A = as_f16x8(reinterpret_cast<const u32x4*>(xrec)[j]);
-        acc_lo = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-            A, as_f16x8(mfma_src(b[8 * j], b[8 * j + 1], b[8 * j + 2], b[8 * j + 3])), acc_lo, 0, 0, 0);
-        acc_hi = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-            A, as_f16x8(mfma_src(b[8 * j + 4], b[8 * j + 5], b[8 * j + 6], b[8 * j + 7])), acc_hi, 0, 0, 0);
+        const int p0 = 16 * (j & 1) + 2 * (j >> 1);
+        mfma(acc_lo, A[j], mfma_src(b[p0], b[p0 + 1], b[p0 + 8], b[p0 + 9]));
+        mfma(acc_hi, A[j], mfma_src(b[p0 + 4], b[p0 + 5], b[p0 + 12], b[p0 + 13]));
       }
     } else {
       uint32_t b[16];
       decode_run<K, CB, false>(st.w, st.wp, b, xor_v);
-      // A fragments: k pairs (0,1) (8,9) (2,3) (10,11) and (4,5) (12,13) (6,7) (14,15) of the k-tile
-      const f16x8 A0 = as_f16x8(u32x4{st.x0.x, st.x1.x, st.x0.y, st.x1.y});
-      const f16x8 A1 = as_f16x8(u32x4{st.x0.z, st.x1.z, st.x0.w, st.x1.w});
-      // positions 16jj + 4half + {0..3} and 16jj + 8 + 4half + {0..3}: registers (8jj + 2half + {0,1}),
-      // (8jj + 4 + 2half + {0,1})
-      acc_lo = __builtin_amdgcn_mfma_f32_16x16x32_f16(A0, as_f16x8(mfma_src(b[0], b[1], b[4], b[5])), acc_lo, 0, 0, 0);
-      acc_hi = __builtin_amdgcn_mfma_f32_16x16x32_f16(A0, as_f16x8(mfma_src(b[2], b[3], b[6], b[7])), acc_hi, 0, 0, 0);
-      acc_lo = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1, as_f16x8(mfma_src(b[8], b[9], b[12], b[13])), acc_lo, 0, 0, 0);
-      acc_hi = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1, as_f16x8(mfma_src(b[10], b[11], b[14], b[15])), acc_hi, 0, 0,
-                                                      0);
+      // A = natural k pairs (0,1) (2,3) (4,5) (6,7) and (8,9) .. (14,15); b[i] holds positions 2i, 2i+1:
+      // k pair (2m, 2m+1) of the lo column is position 8m (m < 4) or 8(m-4) + 2 (m >= 4), hi column + 4
+      mfma(acc_lo, X[0], mfma_src(b[0], b[4], b[8], b[12]));
+      mfma(acc_hi, X[0], mfma_src(b[2], b[6], b[10], b[14]));
+      mfma(acc_lo, X[1], mfma_src(b[1], b[5], b[9], b[13]));
+      mfma(acc_hi, X[1], mfma_src(b[3], b[7], b[11], b[15]));
     }
   };
 
-  // Three prefetch sets rotate without copies, so each wait is for exactly the set about to be used while
-  // the two younger sets stay in flight. Prefetches past the split re-read its last tile (clamped).
-  Stage<K, GA> sa, sb, sc;
-  issue_it(sa, 0);
-  issue_it(sb, 1);
-  issue_it(sc, 2);
-  for (int it = 0;;) {
-    process(sa, it);
-    issue_it(sa, it + 3);
-    if (++it >= iters) break;
-    process(sb, it);
-    issue_it(sb, it + 3);
-    if (++it >= iters) break;
-    process(sc, it);
-    issue_it(sc, it + 3);
-    if (++it >= iters) break;
+  // D phases per trip of a loop with a single back-edge (so the wait before each set is exact: the D-1
+  // younger sets stay in flight), the remaining < D iterations peeled after it. Each phase reads the next
+  // phase's activations from LDS first. Scheduling barriers keep one phase's decode from being hoisted into
+  // the previous one, which would make it wait for a set that is still in flight.
+  u32x4 X[2][2];
+  read_A(0, X[0]);
+  const int full = iters / D * D;
+  int it = 0;
+  for (; it < full; it += D) {
+    static_for<0, D>([&](auto P) {
+      constexpr int d = decltype(P)::value;
+      read_A(it + d + 1, X[(d + 1) & 1]);
+      process(st[d], X[d & 1]);
+      issue_it(st[d], it + d + D);
+      __builtin_amdgcn_sched_barrier(0);
+    });
   }
+  static_for<0, D - 1>([&](auto P) {
+    constexpr int d = decltype(P)::value;
+    if (it + d < iters) {
+      read_A(it + d + 1, X[(d + 1) & 1]);
+      process(st[d], X[d & 1]);
+    }
+  });
 
   // ---- columns of this wavefront -> block partial (LDS) ----
   const int col_lo = (wave * 2 + (c >> 3)) * 16 + g, col_hi = col_lo + 8;
@@ -323,65 +346,60 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
 // ------------------------------------------------------------------------------------------------
 // host side
 // ------------------------------------------------------------------------------------------------
-static bool split_layout(int cb, unsigned flags) { return cb < 2 && (flags & EXL3_GEMV_FAST); }
+// A-operand layout for a codebook and flags: MUL1 always contracts fp16-rounded values (pair layout)
+static int layout_for(int cb, unsigned flags) { return (cb == 2 || !(flags & EXL3_GEMV_FAST)) ? kPair : kSplit; }
 
-constexpr int kResidentWgs = 1024;           // 256 CUs x 4 workgroups of 4 wavefronts (VGPR-limited occupancy)
-constexpr size_t kStageBudget = 48 * 1024;   // LDS bytes for the staged activations of one split (split layout)
+constexpr int kMaxKtPerSplit = 96;           // staged activations of a split stay within 64 KiB at 16 rows
 
-// k-tiles per split. The grid (blocks x S workgroups) is sized to one resident round of workgroups, so no
-// workgroup waits for a second round, with splits as long as that allows (fewer partial sums, longer
-// streams per wavefront). The split depends only on the shape and the activation layout, never on the row
-// count, so each row is summed in the same order whatever the batch (row-exact results). The split
-// layout stages its activations in LDS, which caps its split at the maximum row count.
-static int auto_kt_per_split(int KT, int blocks, bool split) {
-  const int S_occ = blocks >= kResidentWgs ? 1 : kResidentWgs / blocks;
-  int kps = (KT + S_occ - 1) / S_occ;
-  kps = (kps + 3) / 4 * 4;
-  if (split) {
-    const int cap = (int)(kStageBudget / ((size_t)kMaxRows * 16 * 4)) / 4 * 4;
-    if (kps > cap) kps = cap;
-  }
-  return kps < 4 ? 4 : kps;
+// k-tiles per split. Measured on MI355X at K = 6 (27B shapes), the GEMV's time is flat within a few percent
+// for splits of 40-96 k-tiles and grows outside that range: shorter splits add partial sums and pipeline
+// fills, longer ones leave too few workgroups for narrow outputs. Wide outputs (>= 128 blocks of 128
+// columns, 1000+ workgroups at 48) take 48, narrow ones 96. The split depends only on the shape, never on
+// the row count, so each row is summed in the same order whatever the batch (row-exact results).
+static int auto_kt_per_split(int KT, int blocks) {
+  int kps = blocks >= 128 ? 48 : kMaxKtPerSplit;
+  const int ktr = (KT + 3) / 4 * 4;
+  return kps > ktr ? ktr : kps;
 }
 
-// workspace: [per-block counters, padded to 256 B][256 zero bytes][S x rows x n_total fp32 partials]
+// workspace: [per-block counters, padded to 256 B][S x rows x n_total fp32 partials]
 static size_t counters_bytes(int blocks) { return ((size_t)blocks * sizeof(uint32_t) + 255) / 256 * 256; }
 
 static size_t workspace_for(int KT, int blocks, int rows, int n_total, int kps) {
   const int S = (KT + kps - 1) / kps;
-  size_t bytes = counters_bytes(blocks) + 256;
+  size_t bytes = counters_bytes(blocks);
   if (S > 1) bytes += (size_t)S * rows * n_total * sizeof(float);
   return bytes;
 }
 
-template <int K, int CB, bool FAST, int OT>
+template <int K, int CB, int L, int OT>
 static void launch_gemv(const GemvArgs& a, int blocks, size_t smem, hipStream_t st) {
-  gemv_kernel<K, CB, FAST, OT><<<dim3(blocks, a.S), 256, smem, st>>>(a);
+  gemv_kernel<K, CB, L, OT><<<dim3(blocks, a.S), 256, smem, st>>>(a);
 }
 
-template <int K, int CB, bool FAST>
+template <int K, int CB, int L>
 static void dispatch_ot(int ot, const GemvArgs& a, int blocks, size_t smem, hipStream_t st) {
-  if (ot == kF16) launch_gemv<K, CB, FAST, kF16>(a, blocks, smem, st);
-  else if (ot == kBF16) launch_gemv<K, CB, FAST, kBF16>(a, blocks, smem, st);
-  else launch_gemv<K, CB, FAST, kF32>(a, blocks, smem, st);
+  if (ot == kF16) launch_gemv<K, CB, L, kF16>(a, blocks, smem, st);
+  else if (ot == kBF16) launch_gemv<K, CB, L, kBF16>(a, blocks, smem, st);
+  else launch_gemv<K, CB, L, kF32>(a, blocks, smem, st);
 }
 
 template <int K, int CB>
-static void dispatch_fast(bool fast, int ot, const GemvArgs& a, int blocks, size_t smem, hipStream_t st) {
+static void dispatch_layout(int layout, int ot, const GemvArgs& a, int blocks, size_t smem, hipStream_t st) {
   if constexpr (CB < 2) {
-    if (fast) {
-      dispatch_ot<K, CB, true>(ot, a, blocks, smem, st);
+    if (layout == kSplit) {
+      dispatch_ot<K, CB, kSplit>(ot, a, blocks, smem, st);
       return;
     }
   }
-  dispatch_ot<K, CB, false>(ot, a, blocks, smem, st);
+  dispatch_ot<K, CB, kPair>(ot, a, blocks, smem, st);
 }
 
 template <int K>
-static void dispatch_cb(int cb, bool fast, int ot, const GemvArgs& a, int blocks, size_t smem, hipStream_t st) {
-  if (cb == 0) dispatch_fast<K, 0>(fast, ot, a, blocks, smem, st);
-  else if (cb == 1) dispatch_fast<K, 1>(fast, ot, a, blocks, smem, st);
-  else dispatch_fast<K, 2>(fast, ot, a, blocks, smem, st);
+static void dispatch_cb(int cb, int layout, int ot, const GemvArgs& a, int blocks, size_t smem, hipStream_t st) {
+  if (cb == 0) dispatch_layout<K, 0>(layout, ot, a, blocks, smem, st);
+  else if (cb == 1) dispatch_layout<K, 1>(layout, ot, a, blocks, smem, st);
+  else dispatch_layout<K, 2>(layout, ot, a, blocks, smem, st);
 }
 
 }  // namespace exl3
@@ -391,10 +409,7 @@ using namespace exl3;
 extern "C" size_t exl3_gemv_workspace_bytes(int k, int n_total, int rows, int K) {
   if (k <= 0 || k % 16 || n_total <= 0 || n_total % 128 || rows < 1 || rows > kMaxRows || K < 1 || K > 8) return 0;
   const int KT = k / 16, blocks = n_total / 128;
-  // the largest of the two activation layouts' splits
-  const int kps_s = auto_kt_per_split(KT, blocks, true), kps_p = auto_kt_per_split(KT, blocks, false);
-  const size_t a = workspace_for(KT, blocks, rows, n_total, kps_s), b = workspace_for(KT, blocks, rows, n_total, kps_p);
-  return a > b ? a : b;
+  return workspace_for(KT, blocks, rows, n_total, auto_kt_per_split(KT, blocks));
 }
 
 extern "C" int exl3_gemv_ex(const uint16_t* xh, const uint32_t* const* trellis, int n_members, const int* member_n,
@@ -429,10 +444,11 @@ extern "C" int exl3_gemv_ex(const uint16_t* xh, const uint32_t* const* trellis, 
     a.blk_end[i] = 1 << 30;
   }
   const int KT = k / 16, blocks = n_total / 128;
-  const bool split = split_layout(cb, flags);
-  int kps = kt_per_split > 0 ? ((kt_per_split + 3) / 4) * 4 : auto_kt_per_split(KT, blocks, split);
-  EXL3_REQUIRE(!split || ((size_t)kps * rows + 1) * 16 * 4 <= 60 * 1024, EXL3_ERR_ARG,
-               "exl3_gemv: kt_per_split %d too large for %d rows", kps, rows);
+  const int layout = layout_for(cb, flags);
+  const int kps = kt_per_split > 0 ? ((kt_per_split + 3) / 4) * 4 : auto_kt_per_split(KT, blocks);
+  // staged activations: ((iters + 1) * 4 * rows + 1) records of 32 bytes
+  const size_t smem = ((size_t)(kps / 4 + 1) * 4 * rows + 1) * 32;
+  EXL3_REQUIRE(smem <= 64 * 1024, EXL3_ERR_ARG, "exl3_gemv: kt_per_split %d too large for %d rows", kps, rows);
   const int S = (KT + kps - 1) / kps;
   const size_t need = workspace_for(KT, blocks, rows, n_total, kps);
   EXL3_REQUIRE(workspace && workspace_bytes >= need && aligned(workspace, 256), EXL3_ERR_WORKSPACE,
@@ -443,27 +459,23 @@ extern "C" int exl3_gemv_ex(const uint16_t* xh, const uint32_t* const* trellis, 
   a.bias = bias;
   a.y = y;
   a.counters = static_cast<uint32_t*>(workspace);
-  a.xzero = reinterpret_cast<const uint16_t*>(static_cast<char*>(workspace) + counters_bytes(blocks));
-  a.partials = reinterpret_cast<float*>(static_cast<char*>(workspace) + counters_bytes(blocks) + 256);
+  a.partials = reinterpret_cast<float*>(static_cast<char*>(workspace) + counters_bytes(blocks));
   a.k = k;
   a.KT = KT;
   a.rows = rows;
   a.n_total = n_total;
   a.S = S;
   a.kt_per_split = kps;
-  const int iters_max = (kps + 3) / 4;
-  const size_t smem = split ? ((size_t)iters_max * 4 * rows + 1) * 16 * 4 : 0;
-  const bool fast = (flags & EXL3_GEMV_FAST) != 0;
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (K) {
-    case 1: dispatch_cb<1>(cb, fast, out_dtype, a, blocks, smem, st); break;
-    case 2: dispatch_cb<2>(cb, fast, out_dtype, a, blocks, smem, st); break;
-    case 3: dispatch_cb<3>(cb, fast, out_dtype, a, blocks, smem, st); break;
-    case 4: dispatch_cb<4>(cb, fast, out_dtype, a, blocks, smem, st); break;
-    case 5: dispatch_cb<5>(cb, fast, out_dtype, a, blocks, smem, st); break;
-    case 6: dispatch_cb<6>(cb, fast, out_dtype, a, blocks, smem, st); break;
-    case 7: dispatch_cb<7>(cb, fast, out_dtype, a, blocks, smem, st); break;
-    default: dispatch_cb<8>(cb, fast, out_dtype, a, blocks, smem, st); break;
+    case 1: dispatch_cb<1>(cb, layout, out_dtype, a, blocks, smem, st); break;
+    case 2: dispatch_cb<2>(cb, layout, out_dtype, a, blocks, smem, st); break;
+    case 3: dispatch_cb<3>(cb, layout, out_dtype, a, blocks, smem, st); break;
+    case 4: dispatch_cb<4>(cb, layout, out_dtype, a, blocks, smem, st); break;
+    case 5: dispatch_cb<5>(cb, layout, out_dtype, a, blocks, smem, st); break;
+    case 6: dispatch_cb<6>(cb, layout, out_dtype, a, blocks, smem, st); break;
+    case 7: dispatch_cb<7>(cb, layout, out_dtype, a, blocks, smem, st); break;
+    default: dispatch_cb<8>(cb, layout, out_dtype, a, blocks, smem, st); break;
   }
   EXL3_LAUNCH_CHECK("exl3_gemv");
   return EXL3_OK;
