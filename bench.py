@@ -15,8 +15,11 @@ Inputs (rotated activations, trellis, svh) are resident in HBM before timing sta
                  HIP events on the launch stream, against the 8 TB/s HBM3E peak; traffic = HBM bytes per
                  launch from rocprofv3 FETCH_SIZE / WRITE_SIZE (profiles/), or null
   cpu_baseline   the NumPy oracle (reconstruct + fp32 matmul + Hadamard + svh) on the q projection
+  decode_tok_s   end-to-end batch-1 greedy decode of the synthetic 27B-shape EXL3 decoder (config 5: 64
+                 layers, hidden 5120, MLP 17408, GQA 48/8 x 128, head 5120 -> 151936, K = 6): a 512-token
+                 random-id prompt, then 256 tokens, each decode step replayed from one captured HIP graph
 
-    python bench.py [--gpus 1] [--steps 240] [--warmup 24] [--mode exact|fast]
+    python bench.py [--gpus 1] [--steps 240] [--warmup 24] [--mode exact|fast] [--decoder-layers 64]
 """
 from __future__ import annotations
 
@@ -124,6 +127,66 @@ def cpu_baseline(seconds_budget: float = 30.0) -> dict:
     }
 
 
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def decode_benchmark(pk, torch, dev, n_layers: int, prompt: int, gen: int) -> dict:
+    """Config 5: build the synthetic decoder, prefill a random-id prompt, then time `gen` greedy decode
+    steps replayed from one captured HIP graph (inputs, weights and KV cache resident in HBM)."""
+    from omlx_exl3_amd.synthetic import DecoderConfig, SyntheticDecoder, greedy_step
+
+    cfg = DecoderConfig(n_layers=n_layers, max_len=prompt + gen + 8)
+    t0 = time.perf_counter()
+    model = SyntheticDecoder(cfg, seed=2024, device=dev)
+    torch.cuda.synchronize()
+    t_build = time.perf_counter() - t0
+    log(f"decoder built ({n_layers} layers) in {t_build:.1f} s")
+    g = torch.Generator(device=dev).manual_seed(99)
+    ids = torch.randint(0, cfg.vocab, (prompt,), generator=g, device=dev)
+    pos = torch.arange(prompt, device=dev)
+    model(ids, pos)                                      # warm-up prefill (plans, kernels)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    logits = model(ids, pos)
+    torch.cuda.synchronize()
+    t_prefill = time.perf_counter() - t0
+    log(f"prefill of {prompt} tokens: {t_prefill * 1e3:.1f} ms")
+    tok = torch.zeros(1, dtype=torch.int64, device=dev)
+    cur = torch.full((1,), prompt, dtype=torch.int64, device=dev)
+    tok.copy_(greedy_step.argmax(logits).view(1))
+    start_tok, start_pos = tok.clone(), cur.clone()
+    side = torch.cuda.Stream(device=dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        greedy_step(model, tok, cur)                     # eager warm-up step (plans for 1 row, buffers)
+    torch.cuda.current_stream(dev).wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        greedy_step(model, tok, cur)
+    tok.copy_(start_tok)
+    cur.copy_(start_pos)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(gen):
+        graph.replay()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    log(f"{gen} decode steps: {wall * 1e3:.1f} ms")
+    finite = bool(torch.isfinite(model.last_logits).all().item())
+    tok_s = gen / wall
+    L_avg = prompt + gen / 2
+    kv_bytes = n_layers * 2 * cfg.n_kv_heads * cfg.head_dim * 2 * L_avg
+    weights = n_layers * cfg.layer_trellis_bytes() + cfg.head_trellis_bytes()
+    bpt = weights + kv_bytes
+    return {"tok_s": round(tok_s, 2), "ms_per_token": round(wall / gen * 1e3, 3), "layers": n_layers,
+            "prompt": prompt, "gen_tokens": gen, "bytes_per_token": int(bpt),
+            "GB_s": round(bpt * tok_s / 1e9, 1), "pct_hbm_peak": round(100 * bpt * tok_s / 1e9 / HBM_PEAK_GBS, 1),
+            "prefill_tok_s": round(prompt / t_prefill, 1), "build_s": round(t_build, 1),
+            "logits_finite": finite, "fused": model.fused, "sibling_groups": model.groups}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -135,6 +198,9 @@ def main() -> int:
     ap.add_argument("--traffic-file", default=os.path.join(ROOT, "profiles", "gemv_27b_k6_traffic.txt"))
     ap.add_argument("--copy-probe", action="store_true",
                     help="run only a 1 GiB device copy (calibrates rocprofv3 FETCH/WRITE counters)")
+    ap.add_argument("--decoder-layers", type=int, default=64, help="layers of the end-to-end decoder (0 = skip)")
+    ap.add_argument("--prompt", type=int, default=512)
+    ap.add_argument("--gen", type=int, default=256)
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -275,8 +341,17 @@ def main() -> int:
         "per_shape": per_shape,
         "decode_tok_s": None,
     }
+    log(f"GEMV: {value:.1f} GB/s whole job, kernel {kernel_gbs:.1f} GB/s")
+    del layers, evs, graph
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    if args.decoder_layers > 0:
+        dec = decode_benchmark(pk, torch, dev, args.decoder_layers, args.prompt, args.gen)
+        result["decode_tok_s"] = dec["tok_s"]
+        result["decode"] = dec
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline()
+        log("cpu baseline done")
     print(json.dumps(result))
     return 0
 

@@ -8,5 +8,8 @@ The directory is imported under the module name `omlx_exl3_amd`.
 """
 from . import kernels  # noqa: F401
 from ._capi import LIB_PATH, Exl3Error  # noqa: F401
+from .fusion import fuse_decode  # noqa: F401
+from .linear import EXL3Linear, EXL3SiblingGroup, RowExactLinear, unpack_signs  # noqa: F401
+from .loader import group_siblings, inventory, is_exl3_config, load_exl3  # noqa: F401
 
 __version__ = "0.1.0"

@@ -1,0 +1,217 @@
+"""GPU tests of the layer API (EXL3Linear, EXL3SiblingGroup, fusion, loader, the synthetic decoder)
+against the CPU oracle and against each other, through the C ABI.
+
+Bars: max-abs-rel 2e-3 for fp16 / fp32 outputs and 1e-2 for bf16 (exl3_kernel_test.py:50) against the
+fp64 oracle linear; bitwise equality where the same kernels run on the same data (sibling group vs its
+members, graph replay vs eager decode)."""
+import math
+
+import numpy as np
+import pytest
+
+from conftest import load_package
+from oracle import exl3_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+@pytest.fixture(scope="module")
+def pk():
+    return load_package()
+
+
+def _make_linear(pk, k, n, K, cb, seed, bias=False, legacy=False):
+    from omlx_exl3_amd.linear import EXL3Linear
+
+    rng = np.random.default_rng(seed)
+    parts = {"trellis": ((k // 16, n // 16, 16 * K), torch.int16)}
+    if legacy:
+        parts["su"], parts["sv"] = ((k // 16,), torch.int16), ((n // 16,), torch.int16)
+    else:
+        parts["suh"], parts["svh"] = ((k,), torch.float16), ((n,), torch.float16)
+    if cb == 1:
+        parts["mcg"] = ((1,), torch.int16)
+    if cb == 2:
+        parts["mul1"] = ((1,), torch.int16)
+    if bias:
+        parts["bias"] = ((n,), torch.float16)
+    lin = EXL3Linear(k, n, parts, device="cuda")
+    tr = O.random_trellis(k, n, K, seed)
+    lin.trellis.copy_(torch.from_numpy(np.ascontiguousarray(tr).view(np.int16)))
+    if legacy:
+        su = rng.integers(0, 1 << 16, k // 16).astype(np.uint16).view(np.int16)
+        sv = rng.integers(0, 1 << 16, n // 16).astype(np.uint16).view(np.int16)
+        lin.su.copy_(torch.from_numpy(su))
+        lin.sv.copy_(torch.from_numpy(sv))
+        suh, svh = O.unpack_signs(su), O.unpack_signs(sv)
+    else:
+        suh = np.where(rng.integers(0, 2, k) == 1, 1.0, -1.0).astype(np.float16)
+        svh = (rng.standard_normal(n) / math.sqrt(k)).astype(np.float16)
+        lin.suh.copy_(torch.from_numpy(suh))
+        lin.svh.copy_(torch.from_numpy(svh))
+    b = None
+    if bias:
+        b = (rng.standard_normal(n) * 0.1).astype(np.float16)
+        lin.bias.copy_(torch.from_numpy(b))
+    return lin, tr, suh, svh, b
+
+
+def _ref(x, tr, k, n, K, cb, suh, svh, b):
+    xn = x.float().cpu().numpy().reshape(-1, k)
+    return O.linear_ref(xn, tr, k, n, K, cb, suh, svh, b)
+
+
+@pytest.mark.parametrize("legacy,bias,cb", [(False, False, 0), (False, True, 0), (True, False, 1), (True, True, 2)])
+def test_linear_decode_and_prefill_vs_oracle(pk, legacy, bias, cb):
+    k, n, K = 1024, 768, 6
+    lin, tr, suh, svh, b = _make_linear(pk, k, n, K, cb, seed=5 + cb, bias=bias, legacy=legacy)
+    g = torch.Generator(device="cuda").manual_seed(1)
+    for shape in ((1, 1, k), (3, k), (2, 4, k), (4, 10, k)):          # 1, 3, 8 rows: GEMV; 40 rows: prefill
+        for dt, bar in ((torch.float16, 2e-3), (torch.bfloat16, 1e-2), (torch.float32, 2e-3)):
+            x = torch.randn(shape, device="cuda", generator=g).to(dt)
+            y = lin(x)
+            assert y.dtype == dt and tuple(y.shape) == shape[:-1] + (n,)
+            ref = _ref(x, tr, k, n, K, cb, suh, svh, b)
+            e = O.max_abs_rel(y.float().cpu().numpy().reshape(-1, n), ref)
+            assert e < bar, (shape, dt, e)
+
+
+def test_sibling_group_matches_members_bitwise(pk):
+    from omlx_exl3_amd.linear import EXL3SiblingGroup
+
+    k = 1024
+    mk = lambda n, s: _make_linear(pk, k, n, 6, 0, seed=s)[0]  # noqa: E731
+    q, kk, v = mk(512, 1), mk(256, 2), mk(256, 3)
+    g = torch.Generator(device="cuda").manual_seed(2)
+    xs = [torch.randn(r, k, device="cuda", generator=g).half() for r in (1, 3, 20)]
+    alone = [[m(x) for m in (q, kk, v)] for x in xs]
+    grp = EXL3SiblingGroup([q, kk, v])
+    for x, want in zip(xs, alone):
+        got = (q(x), kk(x), v(x))
+        assert grp._cache_x is x
+        for a, w in zip(got, want):
+            assert torch.equal(a, w)
+        if x.shape[0] <= 8:
+            assert torch.equal(torch.cat(got, dim=-1), grp.gemv(x, torch.float16))
+
+
+def _tiny_cfg():
+    from omlx_exl3_amd.synthetic import DecoderConfig
+    return DecoderConfig(n_layers=2, hidden=512, intermediate=1024, n_heads=4, n_kv_heads=2, head_dim=128,
+                         vocab=2048, max_len=64)
+
+
+def test_fused_decoder_matches_unfused_and_saves_rotations(pk, monkeypatch):
+    from omlx_exl3_amd import linear as L
+    from omlx_exl3_amd.synthetic import SyntheticDecoder, greedy_step
+
+    cfg = _tiny_cfg()
+    fused = SyntheticDecoder(cfg, seed=3, device="cuda", fuse=True)
+    plain = SyntheticDecoder(cfg, seed=3, device="cuda", fuse=False)
+    assert fused.fused == {"norm": 4, "mlp": 2, "head": 1} and plain.fused == {}
+    ids = torch.randint(0, cfg.vocab, (12,), device="cuda", generator=torch.Generator(device="cuda").manual_seed(4))
+    pos = torch.arange(12, device="cuda")
+    a, b = fused(ids, pos), plain(ids, pos)                    # prefill (rows > 8): identical paths
+    assert torch.equal(a, b)
+    calls = {"n": 0}
+    real_rot = L.rot
+
+    def counting_rot(*args, **kw):
+        calls["n"] += 1
+        return real_rot(*args, **kw)
+
+    monkeypatch.setattr(L, "rot", counting_rot)
+    ta, pa = torch.tensor([7], device="cuda"), torch.tensor([12], device="cuda")
+    tb, pb = ta.clone(), pa.clone()
+    for _ in range(4):
+        calls["n"] = 0
+        greedy_step(fused, ta, pa)
+        n_fused = calls["n"]
+        calls["n"] = 0
+        greedy_step(plain, tb, pb)
+        n_plain = calls["n"]
+        assert n_fused == cfg.n_layers and n_plain == 4 * cfg.n_layers + 1      # o_proj only vs every consumer
+        la, lb = fused.last_logits, plain.last_logits
+        assert torch.isfinite(la).all()
+        e = ((la - lb).abs().max() / lb.abs().max()).item()
+        assert e < 2e-2, e                                     # SwiGLU fused in fp32 vs fp16 torch ops
+        tb.copy_(ta)                                           # keep both on the same token stream
+
+
+def test_decoder_graph_replay_matches_eager(pk):
+    from omlx_exl3_amd.synthetic import SyntheticDecoder, greedy_step
+
+    cfg = _tiny_cfg()
+    eager = SyntheticDecoder(cfg, seed=5, device="cuda")
+    graphed = SyntheticDecoder(cfg, seed=5, device="cuda")
+    ids = torch.randint(0, cfg.vocab, (16,), device="cuda", generator=torch.Generator(device="cuda").manual_seed(6))
+    pos = torch.arange(16, device="cuda")
+    first = greedy_step.argmax(eager(ids, pos)).view(1)
+    assert torch.equal(first, greedy_step.argmax(graphed(ids, pos)).view(1))
+    te, pe = first.clone(), torch.tensor([16], device="cuda")
+    tg, pg = first.clone(), pe.clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        greedy_step(graphed, tg, pg)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        greedy_step(graphed, tg, pg)
+    tg.copy_(first)
+    pg.fill_(16)
+    for step in range(6):
+        greedy_step(eager, te, pe)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(tg, te) and torch.equal(pg, pe), step
+        assert torch.equal(graphed.last_logits, eager.last_logits), step
+        _ = (torch.randn(4096, device="cuda") * 2).sum().item()      # unrelated eager work between replays
+
+
+def test_loader_end_to_end_on_gpu(pk, tmp_path):
+    from safetensors.torch import save_file
+    from torch import nn
+    from omlx_exl3_amd import loader
+
+    k, nq, nkv, K = 512, 512, 256, 5
+    tensors, refs = {}, {}
+    rng = np.random.default_rng(9)
+    for i, (name, n) in enumerate((("q_proj", nq), ("k_proj", nkv), ("v_proj", nkv))):
+        tr = O.random_trellis(k, n, K, 40 + i)
+        suh = np.where(rng.integers(0, 2, k) == 1, 1.0, -1.0).astype(np.float16)
+        svh = (rng.standard_normal(n) / math.sqrt(k)).astype(np.float16)
+        p = f"layers.0.self_attn.{name}"
+        tensors[f"{p}.trellis"] = torch.from_numpy(np.ascontiguousarray(tr).view(np.int16))
+        tensors[f"{p}.suh"], tensors[f"{p}.svh"] = torch.from_numpy(suh), torch.from_numpy(svh)
+        refs[name] = (tr, n, suh, svh)
+    save_file(tensors, str(tmp_path / "model.safetensors"))
+
+    class Attn(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.q_proj = nn.Linear(k, nq, bias=False)
+            self.k_proj = nn.Linear(k, nkv, bias=False)
+            self.v_proj = nn.Linear(k, nkv, bias=False)
+
+    class Layer(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.self_attn = Attn()
+
+    model = nn.Module()
+    model.layers = nn.ModuleList([Layer()])
+    model = model.cuda()
+    info = loader.load_exl3(model, tmp_path)
+    assert info["linears"] == 3 and info["groups"] == 1
+    att = model.layers[0].self_attn
+    x = torch.randn(2, k, device="cuda").half()
+    for name in ("q_proj", "k_proj", "v_proj"):
+        tr, n, suh, svh = refs[name]
+        y = getattr(att, name)(x)
+        ref = O.linear_ref(x.float().cpu().numpy(), tr, k, n, K, 0, suh, svh)
+        assert O.max_abs_rel(y.float().cpu().numpy(), ref) < 2e-3, name
