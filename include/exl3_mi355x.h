@@ -124,6 +124,24 @@ int exl3_swiglu_rotate(const uint16_t* gu, const uint16_t* suh, int rows, int n,
 int exl3_prefill_gemm(const uint16_t* xh, const uint32_t* trellis, int k, int n, int K, int cb,
                       const uint16_t* svh, const void* bias, void* y, int out_dtype, int rows, void* stream);
 
+/* Batch-1 decode attention producing o_proj's rotated input. No counterpart in the reference, which
+ * fuses rotations into the norm and SwiGLU producers (fusion.py:4-18) but rotates o_proj's input with a
+ * separate rot launch (linear.py:113-116); this entry point applies the same fusion to the attention output
+ * for callers that run the model graph's decode attention on this library (the synthetic decoder).
+ * One launch: rotary embedding of the new q and k (fp32, rotate-half form, then fp16), append k and v at
+ * position *pos to the caches, softmax(q k^T / sqrt(head_dim)) v over positions 0..*pos in fp32, and
+ *   o  = fp16 attention output (n_heads * head_dim), written when o != NULL
+ *   xh = fp16(H128(o * suh) / sqrt(128)) per head (exl3_rotate's arithmetic), written when xh != NULL
+ *   q fp16 [n_heads * 128]; k, v fp16 [n_kv_heads * 128] (the new position's projections)
+ *   k_cache, v_cache fp16 [n_kv_heads, max_len, 128]; pos: device int64 (read by the kernel, so captured
+ *   graphs advance it); rope_cos, rope_sin fp32 [max_len, 64]; suh fp16 [n_heads * 128].
+ * head_dim must be 128, n_heads % n_kv_heads == 0, 1 <= max_len <= 8192. A position outside [0, max_len)
+ * writes nothing to the caches and yields zeros. */
+int exl3_attn_decode_rotate(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* k_cache,
+                            uint16_t* v_cache, const int64_t* pos, const float* rope_cos, const float* rope_sin,
+                            int n_heads, int n_kv_heads, int head_dim, int max_len, const uint16_t* suh,
+                            uint16_t* o, uint16_t* xh, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

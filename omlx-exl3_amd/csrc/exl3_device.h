@@ -217,4 +217,30 @@ __device__ __forceinline__ float round_through(float v) {
   else return v;
 }
 
+// 128-point FWHT of the block held by the 16-lane group of this lane (8 consecutive elements per lane):
+// stages h = 1, 2, 4 in-lane, 8..64 across lanes (xor 1, 2, 4, 8), each as (a + b, a - b) in fp32, in the
+// order 1, 2, ..., 64 of the reference's FWHT (kernels.py:374-386).
+__device__ __forceinline__ void fwht128_lane8(float (&e)[8], int lane) {
+#pragma unroll
+  for (int h = 1; h < 8; h <<= 1) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if ((i & h) == 0) {
+        const float a = e[i], b = e[i + h];
+        e[i] = a + b;
+        e[i + h] = a - b;
+      }
+    }
+  }
+#pragma unroll
+  for (int hl = 1; hl < 16; hl <<= 1) {
+    const bool upper = (lane & hl) != 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float p = __shfl_xor(e[i], hl);
+      e[i] = upper ? p - e[i] : e[i] + p;
+    }
+  }
+}
+
 }  // namespace exl3

@@ -13,30 +13,6 @@
 
 namespace exl3 {
 
-// 128-point FWHT of the block held by the 16-lane group of this lane (8 elements per lane).
-__device__ __forceinline__ void fwht128_lane8(float (&e)[8], int lane) {
-#pragma unroll
-  for (int h = 1; h < 8; h <<= 1) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      if ((i & h) == 0) {
-        const float a = e[i], b = e[i + h];
-        e[i] = a + b;
-        e[i + h] = a - b;
-      }
-    }
-  }
-#pragma unroll
-  for (int hl = 1; hl < 16; hl <<= 1) {
-    const bool upper = (lane & hl) != 0;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float p = __shfl_xor(e[i], hl);
-      e[i] = upper ? p - e[i] : e[i] + p;
-    }
-  }
-}
-
 template <int DT>
 __device__ __forceinline__ void load8(const void* base, size_t i0, float (&v)[8]) {
   if constexpr (DT == kF32) {
@@ -121,10 +97,13 @@ __global__ __launch_bounds__(256) void rot_kernel(const void* __restrict__ x, co
   rotate_members(xv, suh, nm, rows, r, k, c0, xh, lane, valid);
 }
 
-// One workgroup per row. Sum of squares accumulated in fp64: the squares of fp16/bf16 values are exact in
-// fp64 and the sum is exact for any realistic activation range, so the result does not depend on the
-// reduction order; it is then rounded once to fp32 and put through the reference's fp32 steps
-// (mean = ss / KD, + eps) and a correctly rounded reciprocal square root (kernels.py:421).
+// grid (ceil(k / 2048), rows): workgroup (s, r) normalises and rotates elements [2048 s, 2048 s + 2048) of
+// row r, one 128-block per 16-lane group. Every workgroup of a row first computes the row's sum of squares
+// itself (the row is a few KiB, read from L2), so a decode step's single row is spread over k / 2048
+// workgroups without a second pass. The sum is accumulated in fp64: the squares of fp16/bf16 values are
+// exact in fp64 and the sum is exact for any realistic activation range, so every workgroup gets the same
+// value whatever its reduction order; it is then rounded once to fp32 and put through the reference's fp32
+// steps (mean = ss / KD, + eps) and a correctly rounded reciprocal square root (kernels.py:421).
 template <int DT>
 __global__ __launch_bounds__(256) void norm_rot_kernel(const void* __restrict__ x, const void* __restrict__ res,
                                                        void* __restrict__ res_out, const void* __restrict__ w,
@@ -133,7 +112,7 @@ __global__ __launch_bounds__(256) void norm_rot_kernel(const void* __restrict__ 
                                                        uint16_t* __restrict__ xh) {
   __shared__ double part[4];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int r = blockIdx.x;
+  const int r = blockIdx.y;
   const int nchunk = k / 8;
   const size_t rowoff = (size_t)r * k;
 
@@ -151,7 +130,6 @@ __global__ __launch_bounds__(256) void norm_rot_kernel(const void* __restrict__ 
   for (int ch = tid; ch < nchunk; ch += 256) {
     float hv[8];
     load_h((size_t)ch * 8, hv);
-    if (res && res_out) store8<DT>(res_out, rowoff + (size_t)ch * 8, hv);
 #pragma unroll
     for (int i = 0; i < 8; ++i) ss += (double)hv[i] * (double)hv[i];
   }
@@ -164,17 +142,18 @@ __global__ __launch_bounds__(256) void norm_rot_kernel(const void* __restrict__ 
   const float v = mean + eps;
   const float inv = (float)(1.0 / sqrt((double)v));
 
-  // 16-lane groups walk the 128-blocks; all lanes of a wavefront iterate together (uniform trip count)
+  // this workgroup's 16 blocks of 128, one per 16-lane group
   const int group = tid >> 4;
   const int nblk = k / 128;
-  for (int b0 = 0; b0 < nblk; b0 += 16) {
-    const int b = b0 + group;
+  {
+    const int b = blockIdx.x * 16 + group;
     const bool valid = b < nblk;
     const size_t c0 = (size_t)b * 128 + (size_t)(tid & 15) * 8;
     float xv[8];
     if (valid) {
       float hv[8], wv[8];
       load_h(c0, hv);
+      if (res && res_out) store8<DT>(res_out, rowoff + c0, hv);
       load8<DT>(w, c0, wv);
 #pragma unroll
       for (int i = 0; i < 8; ++i) xv[i] = round_through<DT>(wv[i] * round_through<DT>(hv[i] * inv));
@@ -253,11 +232,13 @@ extern "C" int exl3_rmsnorm_rotate(const void* x, const void* residual, void* re
                    (!residual_out || aligned(residual_out, 16)) && (!suh || aligned(suh, 16)) &&
                    (!xh || aligned(xh, 16)),
                EXL3_ERR_ARG, "exl3_rmsnorm_rotate: buffers must be 16-byte aligned");
+  EXL3_REQUIRE(rows <= 65535, EXL3_ERR_ARG, "exl3_rmsnorm_rotate: rows must be <= 65535 (got %d)", rows);
   hipStream_t st = static_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)((k + 2047) / 2048), (unsigned)rows);
   if (dtype == kF16)
-    norm_rot_kernel<kF16><<<rows, 256, 0, st>>>(x, residual, residual_out, w, eps, suh, n_members, rows, k, xn, xh);
+    norm_rot_kernel<kF16><<<grid, 256, 0, st>>>(x, residual, residual_out, w, eps, suh, n_members, rows, k, xn, xh);
   else
-    norm_rot_kernel<kBF16><<<rows, 256, 0, st>>>(x, residual, residual_out, w, eps, suh, n_members, rows, k, xn, xh);
+    norm_rot_kernel<kBF16><<<grid, 256, 0, st>>>(x, residual, residual_out, w, eps, suh, n_members, rows, k, xn, xh);
   EXL3_LAUNCH_CHECK("exl3_rmsnorm_rotate");
   return EXL3_OK;
 }

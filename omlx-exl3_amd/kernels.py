@@ -197,5 +197,35 @@ def prefill_gemm(xh: torch.Tensor, trellis: torch.Tensor, k: int, n: int, K: int
     return out
 
 
+def attn_decode_rotate(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, k_cache: torch.Tensor,
+                       v_cache: torch.Tensor, pos: torch.Tensor, rope_cos: torch.Tensor, rope_sin: torch.Tensor,
+                       suh: torch.Tensor | None, want_o: bool = False):
+    """Batch-1 decode attention with rotary embedding and KV-cache append, producing o_proj's rotated input
+    (exl3_attn_decode_rotate). q (n_heads*128,), k / v (n_kv*128,) fp16 (views of one row are fine);
+    caches fp16 (n_kv, max_len, 128); pos int64 (1,) on the device; rope tables fp32 (max_len, 64).
+    Returns (xh (1, 1, n_heads*128) or None, o (1, n_heads*128) or None)."""
+    for t, name in ((k_cache, "k_cache"), (v_cache, "v_cache"), (rope_cos, "rope_cos"), (rope_sin, "rope_sin")):
+        _dev(t, name)
+    n_kv, max_len, hd = k_cache.shape
+    _require(hd == 128 and tuple(v_cache.shape) == (n_kv, max_len, hd), "attn_decode_rotate: caches (n_kv, L, 128)")
+    _require(k_cache.dtype == v_cache.dtype == torch.float16, "attn_decode_rotate: fp16 caches")
+    _require(rope_cos.dtype == rope_sin.dtype == torch.float32 and tuple(rope_cos.shape) == (max_len, 64)
+             and tuple(rope_sin.shape) == (max_len, 64), "attn_decode_rotate: fp32 rope tables (max_len, 64)")
+    _require(pos.dtype == torch.int64 and pos.numel() == 1 and pos.is_cuda, "attn_decode_rotate: int64 pos on device")
+    for t in (q, k, v):
+        _require(t.is_cuda and t.dtype == torch.float16 and t.stride(-1) == 1, "attn_decode_rotate: fp16 q/k/v")
+    n_heads = q.numel() // hd
+    _require(k.numel() == v.numel() == n_kv * hd and n_heads % n_kv == 0, "attn_decode_rotate: head counts")
+    xh = torch.empty((1, 1, n_heads * hd), dtype=torch.float16, device=q.device) if suh is not None else None
+    o = torch.empty((1, n_heads * hd), dtype=torch.float16, device=q.device) if want_o else None
+    if suh is not None:
+        _require(suh.dtype == torch.float16 and suh.numel() == n_heads * hd and suh.is_contiguous(),
+                 "attn_decode_rotate: suh fp16 (n_heads*128,)")
+    check(lib().exl3_attn_decode_rotate(ptr(q), ptr(k), ptr(v), ptr(k_cache), ptr(v_cache), ptr(pos), ptr(rope_cos),
+                                        ptr(rope_sin), n_heads, n_kv, hd, max_len, ptr(suh), ptr(o), ptr(xh),
+                                        stream_handle(q.device)), "exl3_attn_decode_rotate")
+    return xh, o
+
+
 __all__ = ["MAX_GEMV_ROWS", "GEMV_ROWS_LIMIT", "TrellisGemvPlan", "decode_wt", "rot", "norm_rot", "swiglu_rot",
-           "prefill_gemm", "codebook", "Exl3Error"]
+           "prefill_gemm", "codebook", "attn_decode_rotate", "Exl3Error"]

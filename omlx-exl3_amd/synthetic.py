@@ -12,7 +12,9 @@ device generator; suh = +-1, svh = +-1/sqrt(in_features), so that each projectio
 Decode runs with a static KV cache (capacity `max_len`) and a device-side position, so one decode step
 has fixed shapes and can be captured in a HIP graph and replayed. The residual add is fused into the
 RMSNorm kernel (exl3_rmsnorm_rotate with a residual), which also writes the consumers' rotated inputs.
-Attention itself uses torch operations on fp16 tensors (it is not part of the EXL3 path).
+Decode attention is one kernel (exl3_attn_decode_rotate: rotary embedding, cache append, attention and
+o_proj's input rotation); `fused_attn=False` selects the same attention as torch operations instead.
+Prefill attention uses torch operations on fp16 tensors.
 """
 from __future__ import annotations
 
@@ -24,7 +26,7 @@ import torch.nn.functional as F
 from torch import nn
 
 from .fusion import fuse_decode
-from .kernels import MAX_GEMV_ROWS, norm_rot
+from .kernels import MAX_GEMV_ROWS, attn_decode_rotate, norm_rot
 from .linear import EXL3Linear
 from .loader import group_siblings
 
@@ -111,33 +113,37 @@ class Attention(nn.Module):
         self.k_proj = random_exl3_linear(h, kv, cfg.K, cfg.codebook, gen, device)
         self.v_proj = random_exl3_linear(h, kv, cfg.K, cfg.codebook, gen, device)
         self.o_proj = random_exl3_linear(q, h, cfg.K, cfg.codebook, gen, device)
-        # K cache stored transposed (kv_heads, head_dim, max_len) so both attention products read
-        # contiguous operands
-        self.register_buffer("k_cache", torch.zeros(cfg.n_kv_heads, cfg.head_dim, cfg.max_len,
+        self.fused_attn = True
+        self.register_buffer("k_cache", torch.zeros(cfg.n_kv_heads, cfg.max_len, cfg.head_dim,
                                                     dtype=torch.float16, device=device), persistent=False)
         self.register_buffer("v_cache", torch.zeros(cfg.n_kv_heads, cfg.max_len, cfg.head_dim,
                                                     dtype=torch.float16, device=device), persistent=False)
 
-    def forward(self, x, pos, cos, sin):
+    def forward(self, x, pos, cos, sin, cos_half=None, sin_half=None):
         """x (T, hidden) fp16 at positions pos (T,) int64 (device). Decode (T = 1) attends over the cache
-        with a mask; prefill (T > 1) attends causally over the T new positions starting at pos[0] = 0."""
+        up to pos; prefill (T > 1) attends causally over the T new positions starting at pos[0] = 0."""
         cfg = self.cfg
         T = x.shape[0]
         q, k, v = self.q_proj(x), self.k_proj(x), self.v_proj(x)
         nh, nkv, hd = cfg.n_heads, cfg.n_kv_heads, cfg.head_dim
+        if T == 1 and self.fused_attn and cos_half is not None:
+            xh, _ = attn_decode_rotate(q.reshape(-1), k.reshape(-1), v.reshape(-1), self.k_cache, self.v_cache, pos,
+                                       cos_half, sin_half, self.o_proj.rot_suh.reshape(-1))
+            return self.o_proj.gemv_rotated(xh, x.dtype, self.o_proj._bias_for(x.dtype))
         c, s = cos[pos].unsqueeze(1), sin[pos].unsqueeze(1)                       # (T, 1, hd)
         q = q.view(T, nh, hd).float()
         k = k.view(T, nkv, hd).float()
         q = (q * c + _rotate_half(q) * s).to(torch.float16)
         k = (k * c + _rotate_half(k) * s).to(torch.float16)
         v = v.view(T, nkv, hd)
-        self.k_cache.index_copy_(2, pos, k.permute(1, 2, 0).contiguous())
+        self.k_cache.index_copy_(1, pos, k.permute(1, 0, 2).contiguous())
         self.v_cache.index_copy_(1, pos, v.permute(1, 0, 2).contiguous())
         g = nh // nkv
         scale = 1.0 / math.sqrt(hd)
         if T == 1:
             qg = q.view(nkv, g, hd)                                                # (nkv, g, hd)
-            sc = torch.bmm(qg, self.k_cache).float() * scale                       # (nkv, g, L)
+            kt = self.k_cache.transpose(1, 2).contiguous()                         # (nkv, hd, L)
+            sc = torch.bmm(qg, kt).float() * scale                                 # (nkv, g, L)
             mask = torch.arange(cfg.max_len, device=x.device) > pos[0]
             sc = sc.masked_fill(mask, float("-inf"))
             p = torch.softmax(sc, dim=-1).to(torch.float16)
@@ -145,7 +151,7 @@ class Attention(nn.Module):
             o = o.reshape(1, nh * hd)
         else:
             qh = q.permute(1, 0, 2).reshape(nkv, g * T, hd).contiguous()           # (nkv, g*T, hd)
-            kt = self.k_cache[:, :, :T].contiguous()                               # (nkv, hd, T)
+            kt = self.k_cache[:, :T, :].transpose(1, 2).contiguous()               # (nkv, hd, T)
             sc = torch.bmm(qh, kt).float().view(nkv, g, T, T) * scale
             causal = torch.ones(T, T, dtype=torch.bool, device=x.device).triu(1)
             sc = sc.masked_fill(causal, float("-inf"))
@@ -198,7 +204,7 @@ class SyntheticDecoder(nn.Module):
     """The synthetic EXL3 decoder (module docstring). `forward(ids, pos)` runs T tokens at positions pos
     and returns the logits of the last one (vocab,) in fp32."""
 
-    def __init__(self, cfg: DecoderConfig, seed: int = 0, device="cuda", fuse: bool = True):
+    def __init__(self, cfg: DecoderConfig, seed: int = 0, device="cuda", fuse: bool = True, fused_attn: bool = True):
         super().__init__()
         self.cfg = cfg
         gen = torch.Generator(device=device)
@@ -214,9 +220,14 @@ class SyntheticDecoder(nn.Module):
         cos, sin = _rope_tables(cfg, device)
         self.register_buffer("rope_cos", cos, persistent=False)
         self.register_buffer("rope_sin", sin, persistent=False)
+        half = cfg.head_dim // 2      # cos / sin repeat across the two halves of a head (rotate-half form)
+        self.register_buffer("rope_cos_half", cos[:, :half].contiguous(), persistent=False)
+        self.register_buffer("rope_sin_half", sin[:, :half].contiguous(), persistent=False)
         self.requires_grad_(False)
         self.groups = group_siblings(self)
         self.fused = fuse_decode(self) if fuse else {}
+        for layer in self.model.layers:
+            layer.self_attn.fused_attn = fused_attn
 
     @torch.no_grad()
     def forward(self, ids: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
@@ -224,7 +235,7 @@ class SyntheticDecoder(nn.Module):
         residual = None
         for layer in self.model.layers:
             xn, residual = add_rms_norm(layer.input_layernorm, x, residual)
-            x = layer.self_attn(xn, pos, self.rope_cos, self.rope_sin)
+            x = layer.self_attn(xn, pos, self.rope_cos, self.rope_sin, self.rope_cos_half, self.rope_sin_half)
             xn, residual = add_rms_norm(layer.post_attention_layernorm, x, residual)
             x = layer.mlp(xn)
         xn, _ = add_rms_norm(self.model.norm, x, residual)

@@ -6,6 +6,8 @@ fp64 reference, the reference's own bars (exl3_kernel_test.py:50). Full 27B-clas
 through size-independent properties: GEMV == (bit-exact reconstruct, fp32 matmul, Hadamard, svh);
 bitwise determinism; row-exactness (row r identical for any row count).
 """
+import math
+
 import numpy as np
 import pytest
 
@@ -269,3 +271,58 @@ def test_prefill_27b_shape_vs_reconstruct(pk):
     ref = _had128_t(xh.float() @ W.T) * svh.float()
     y = pk.kernels.prefill_gemm(xh, tr, k, n, K, 0, svh, out_dtype=torch.float32)
     assert ((y - ref).abs().max() / ref.abs().max()).item() < 2e-3
+
+
+# ------------------------------------------------------------------------------------------ decode attention
+def _rope_ref(x, c, s):
+    """torch formulation in fp32 with separate roundings: x*cos + rotate_half(x)*sin, then fp16."""
+    h = x.shape[-1] // 2
+    rh = torch.cat((-x[..., h:], x[..., :h]), dim=-1)
+    cc, ss = torch.cat((c, c), dim=-1), torch.cat((s, s), dim=-1)
+    return (x * cc + rh * ss).half()
+
+
+@pytest.mark.parametrize("n_heads,n_kv,pos", [(48, 8, 37), (4, 2, 0), (8, 8, 255), (6, 1, 100)])
+def test_attn_decode_rotate_vs_torch(pk, n_heads, n_kv, pos):
+    """Decode attention kernel: cache append bit-exact vs the torch rope formulation, o within 2e-3 of an
+    fp32 torch attention, xh bit-exact vs the rotation kernel applied to o, other cache rows untouched."""
+    hd, max_len = 128, 256
+    g = torch.Generator(device="cuda").manual_seed(pos + n_heads)
+    q = torch.randn(n_heads * hd, device="cuda", generator=g).half()
+    k = torch.randn(n_kv * hd, device="cuda", generator=g).half()
+    v = torch.randn(n_kv * hd, device="cuda", generator=g).half()
+    kc = torch.randn(n_kv, max_len, hd, device="cuda", generator=g).half()
+    vc = torch.randn(n_kv, max_len, hd, device="cuda", generator=g).half()
+    kc0, vc0 = kc.clone(), vc.clone()
+    ang = torch.rand(max_len, hd // 2, device="cuda", generator=g) * 6.0
+    cos, sin = ang.cos().contiguous(), ang.sin().contiguous()
+    suh = torch.where(torch.rand(n_heads * hd, device="cuda", generator=g) < 0.5, -1.0, 1.0).half()
+    p = torch.tensor([pos], dtype=torch.int64, device="cuda")
+    xh, o = pk.kernels.attn_decode_rotate(q, k, v, kc, vc, p, cos, sin, suh, want_o=True)
+    # reference
+    qr = _rope_ref(q.view(n_heads, hd).float(), cos[pos], sin[pos])
+    kr = _rope_ref(k.view(n_kv, hd).float(), cos[pos], sin[pos])
+    assert torch.equal(kc[:, pos], kr) and torch.equal(vc[:, pos], v.view(n_kv, hd))
+    mask = torch.ones(max_len, dtype=torch.bool, device="cuda")
+    mask[pos] = False
+    assert torch.equal(kc[:, mask], kc0[:, mask]) and torch.equal(vc[:, mask], vc0[:, mask])
+    grp = n_heads // n_kv
+    kf, vf = kc[:, : pos + 1].float(), vc[:, : pos + 1].float()
+    sc = torch.matmul(qr.float().view(n_kv, grp, hd), kf.transpose(1, 2).contiguous()) / math.sqrt(hd)
+    ref = torch.matmul(torch.softmax(sc, dim=-1), vf.contiguous()).reshape(-1)
+    e = ((o.float().view(-1) - ref).abs().max() / ref.abs().max()).item()
+    assert e < 2e-3, e
+    assert torch.equal(xh.view(1, -1), pk.kernels.rot(o, suh.view(1, -1)).view(1, -1))
+
+
+def test_attn_decode_out_of_range_position_writes_nothing(pk):
+    hd, max_len, nh, nkv = 128, 64, 4, 2
+    z = lambda *s: torch.ones(*s, device="cuda").half()  # noqa: E731
+    kc, vc = z(nkv, max_len, hd), z(nkv, max_len, hd)
+    cos = torch.ones(max_len, 64, device="cuda")
+    sin = torch.zeros(max_len, 64, device="cuda")
+    for bad in (max_len, -1):
+        p = torch.tensor([bad], dtype=torch.int64, device="cuda")
+        xh, o = pk.kernels.attn_decode_rotate(z(nh * hd), z(nkv * hd), z(nkv * hd), kc, vc, p, cos, sin,
+                                              z(nh * hd), want_o=True)
+        assert (o == 0).all() and (xh == 0).all() and (kc == 1).all() and (vc == 1).all()
