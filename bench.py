@@ -193,6 +193,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=240)
     ap.add_argument("--warmup", type=int, default=24)
     ap.add_argument("--mode", choices=["exact", "fast"], default="exact")
+    ap.add_argument("--table", action="store_true",
+                    help="the table GEMV kernel (LDS codebook lookup for half of each run) instead of hashing")
     ap.add_argument("--layers", type=int, default=6, help="distinct layers in the rotating working set")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--traffic-file", default=os.path.join(ROOT, "profiles", "gemv_27b_k6_traffic.txt"))
@@ -240,7 +242,8 @@ def main() -> int:
                    for n in ns]
             svh = torch.where(torch.rand(sum(ns), device=dev, generator=g) < 0.5, -1.0, 1.0).half()
             xh = torch.randn((len(ns), rows, k), device=dev, generator=g).half()
-            plan = pk.kernels.TrellisGemvPlan(k, ns, K, cb, svh, rows, torch.float16, fast=fast)
+            plan = pk.kernels.TrellisGemvPlan(k, ns, K, cb, svh, rows, torch.float16, fast=fast,
+                                              table=args.table)
             out = torch.empty((rows, sum(ns)), dtype=torch.float16, device=dev)
             items.append((name, plan, xh, trs, out, algorithmic_bytes(k, ns, K, rows)))
         layers.append(items)
@@ -331,6 +334,7 @@ def main() -> int:
                                 "5120->6144+1024+1024, o 6144->5120, gate_up 5120->17408+17408, down 17408->5120; "
                                 f"{L} distinct layers rotated ({step_bytes * L / 1e9:.2f} GB of weights)"),
                    "global_batch": rows, "bpw": K, "codebook": "3inst", "gemv_mode": args.mode,
+                   "gemv_kernel": "table" if (args.table and not fast) else "hash",
                    "parallelism": "none (1 GPU)"},
         "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 1),
         "roofline": {"bound": "hbm", "achieved": round(kernel_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",

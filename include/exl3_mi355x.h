@@ -46,6 +46,12 @@ extern "C" {
 #define EXL3_GEMV_EXACT 0u      /* contract fp16-rounded codebook values (the reference's arithmetic) */
 #define EXL3_GEMV_FAST 1u       /* 3INST/MCG: contract the two fp16 summands of each codebook value
                                    separately (the unrounded value), one VALU op less per weight */
+#define EXL3_GEMV_TABLE 2u      /* with EXACT and k % 64 == 0: the table kernel, 1024-thread workgroups that
+                                   decode half of each run through an LDS copy of the codebook's lookup table
+                                   (same values, ~25% less VALU work per weight, but a table set-up and more
+                                   split-K traffic per launch; slower than the default hashing kernel on the
+                                   27B decode shapes as measured). Default: every weight decoded by hashing,
+                                   one workgroup per 128-column block and k-split */
 
 /* Library version, (major << 16) | (minor << 8) | patch. */
 int exl3_version(void);
@@ -55,8 +61,9 @@ const char* exl3_last_error(void);
 
 /* Codebook diagnostic: out[s] = fp16 bits of the codebook value of state s, s = 0..65535, evaluated by
  * the same device code the GEMV and reconstruct kernels use (state read from the low half of a word
- * when `hi_half` is 0, from the high half otherwise). Replaces the reference's dec1<CB>
- * (kernels.py:35-48) as a testable unit. out: uint16[65536]. */
+ * when `hi_half` is 0, from the high half when 1), or copied from the lookup table the table GEMV
+ * kernel uses (`hi_half` = 2). Replaces the reference's dec1<CB> (kernels.py:35-48) as a testable unit.
+ * out: uint16[65536]. */
 int exl3_codebook(int cb, int hi_half, uint16_t* out, void* stream);
 
 /* Trellis -> W_inner^T, columns [16*nt0, 16*(nt0+ntc)) of W_inner as a (16*ntc, k) fp16 matrix, bit-exact.
@@ -66,9 +73,10 @@ int exl3_codebook(int cb, int hi_half, uint16_t* out, void* stream);
 int exl3_reconstruct(const uint32_t* trellis, int k, int n, int K, int cb, int nt0, int ntc,
                      uint16_t* w_out, void* stream);
 
-/* Workspace bytes exl3_gemv needs for this shape (deterministic split-K partials + per-block arrival
- * counters). The workspace must be zero-filled once before its first use; every call leaves the
- * counters at zero again. One workspace must not be used by two calls in flight at the same time. */
+/* Workspace bytes exl3_gemv needs for this shape, for either kernel (deterministic split-K partials +
+ * per-block arrival counters). The workspace must be zero-filled once before its first use; every call
+ * leaves the counters at zero again. One workspace must not be used by two calls in flight at the same
+ * time. */
 size_t exl3_gemv_workspace_bytes(int k, int n_total, int rows, int K);
 
 /* Fused decode GEMV: y = had128(xh_m @ W_inner_m) * svh (+ bias) for 1..3 sibling members sharing k, K

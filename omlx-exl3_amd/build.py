@@ -25,6 +25,8 @@ HIPCC_FLAGS = [
     # packed fp32 VALU forms are kept out of the generated code
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-command-line-argument",
+    # the codebook lookup tables are evaluated at compile time (65,536 entries each)
+    "-fconstexpr-steps=50000000",
 ]
 
 

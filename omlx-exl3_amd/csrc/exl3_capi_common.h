@@ -34,4 +34,7 @@ void set_error(const char* fmt, ...);
 
 inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
+// Device address of codebook cb's 65,536-entry fp16 lookup table on the current device (nullptr on failure).
+const uint16_t* codebook_table(int cb);
+
 }  // namespace exl3

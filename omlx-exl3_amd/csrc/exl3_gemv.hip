@@ -24,115 +24,9 @@
 // reproducible, and row r's result does not depend on the number of rows.
 #include "exl3_capi_common.h"
 #include "exl3_device.h"
+#include "exl3_gemv_common.h"
 
 namespace exl3 {
-
-struct GemvArgs {
-  const uint16_t* xh;
-  const uint32_t* tr[3];
-  int NT[3];
-  int blk_end[3];
-  const uint16_t* svh;
-  const void* bias;
-  void* y;
-  float* partials;
-  uint32_t* counters;
-  int k, KT, rows, n_total, S, kt_per_split;
-};
-
-constexpr int kMaxRows = 16;
-constexpr int kBufferFlags = 0x00020000;   // raw buffer descriptor word 3 (32-bit data, no swizzle) for gfx950
-
-__device__ __forceinline__ uint32_t bitop_split(uint32_t h, uint32_t mask_s, uint32_t xor_v) {
-  uint32_t u;
-  asm("v_bitop3_b32 %0, %1, %2, %3 bitop3:0x6a" : "=v"(u) : "v"(h), "s"(mask_s), "v"(xor_v));   // (h & M) ^ X
-  return u;
-}
-
-// Decode one run (32 positions) of K words + the word before into MFMA B registers.
-//   SPLIT: b[p] = (a_p, b_p) fp16 summands, p = 0..31
-//   pair : b[p/2] = (w_p, w_{p+1}) fp16, p even, 16 registers
-template <int K, int CB, bool SPLIT>
-__device__ __forceinline__ void decode_run(const uint32_t* w, uint32_t wp, uint32_t* b, uint32_t xor_v) {
-  if constexpr (SPLIT) {
-    static_for<0, 32>([&](auto P) {
-      constexpr int p = decltype(P)::value;
-      b[p] = bitop_split(hash_pos<CB, K, p>(w, wp), kMask3, xor_v);
-    });
-  } else if constexpr (CB == 2) {
-    static_for<0, 16>([&](auto P) {
-      constexpr int p = 2 * decltype(P)::value;
-      b[p / 2] = mul1_pair(mul1_r(hash_pos<CB, K, p>(w, wp)), mul1_r(hash_pos<CB, K, p + 1>(w, wp)));
-    });
-  } else {
-    static_for<0, 16>([&](auto P) {
-      constexpr int p = 2 * decltype(P)::value;
-      b[p / 2] = sum_pairs(bitop_split(hash_pos<CB, K, p>(w, wp), kMask3, xor_v),
-                           bitop_split(hash_pos<CB, K, p + 1>(w, wp), kMask3, xor_v));
-    });
-  }
-}
-
-// Buffer loads of a run's K stream words (at byte offset vo) and the word before the run (at vo_wp), both
-// advanced by the wave-uniform soff. The workgroup's buffer descriptor ends at the end of its k-split, so
-// prefetches past the split return zeros without touching memory.
-template <int K>
-__device__ __forceinline__ void load_run(__amdgpu_buffer_rsrc_t rs, uint32_t vo, uint32_t vo_wp, uint32_t soff,
-                                         uint32_t* w, uint32_t& wp) {
-  int i = 0;
-#pragma unroll
-  for (; i + 4 <= K; i += 4) {
-    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, vo + 4 * i, soff, 0);
-    w[i] = v.x; w[i + 1] = v.y; w[i + 2] = v.z; w[i + 3] = v.w;
-  }
-  if constexpr (K % 4 == 3) {
-    const u32x3 v = __builtin_amdgcn_raw_buffer_load_b96(rs, vo + 4 * (K - 3), soff, 0);
-    w[K - 3] = v.x; w[K - 2] = v.y; w[K - 1] = v.z;
-  } else if constexpr (K % 4 == 2) {
-    const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rs, vo + 4 * (K - 2), soff, 0);
-    w[K - 2] = v.x; w[K - 1] = v.y;
-  } else if constexpr (K % 4 == 1) {
-    w[K - 1] = __builtin_amdgcn_raw_buffer_load_b32(rs, vo + 4 * (K - 1), soff, 0);
-  }
-  wp = __builtin_amdgcn_raw_buffer_load_b32(rs, vo_wp, soff, 0);
-}
-
-template <typename T>
-__device__ __forceinline__ f16x8 as_f16x8(const T& v) { return __builtin_bit_cast(f16x8, v); }
-
-// The B operands are produced by inline asm, which the compiler's hazard tracking does not count as VALU
-// writes, so it would not insert the wait states an MFMA needs after a VALU write of its source VGPRs.
-// This barrier re-defines the four registers after two wait states (s_nop 1): the MFMA then reads values
-// whose last real writer is at least two instructions back, and the data dependence keeps the decode asm
-// from being scheduled past it.
-__device__ __forceinline__ u32x4 mfma_src(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
-  asm volatile("s_nop 1" : "+v"(a), "+v"(b), "+v"(c), "+v"(d));
-  return u32x4{a, b, c, d};
-}
-
-// Activation (A operand) layouts of the kernel:
-//   kPair   B registers hold two fp16-rounded codebook values (k pair); A = xh's natural fp16 pairs
-//   kSplit  B registers hold the two fp16 summands of one value; A = each activation twice, built from the
-//           natural pairs with byte permutes (2 instructions per k pair)
-enum Layout : int { kPair = 0, kSplit = 1 };
-
-// One trellis prefetch set of a lane: its run's K stream words and the word before the run.
-template <int K>
-struct Stage {
-  uint32_t w[K];
-  uint32_t wp;
-};
-
-__device__ __forceinline__ u32x4 dup4(uint32_t d0, uint32_t d1) {   // (x0,x1),(x2,x3) -> x0 x0, x1 x1, x2 x2, x3 x3
-  return u32x4{__builtin_amdgcn_perm(d0, d0, 0x01000100u), __builtin_amdgcn_perm(d0, d0, 0x03020302u),
-               __builtin_amdgcn_perm(d1, d1, 0x01000100u), __builtin_amdgcn_perm(d1, d1, 0x03020302u)};
-}
-
-// Trellis sets in flight per lane. Decoding keeps the VALU busy for ~1 us per set per SIMD, so only the
-// sets queued behind the one being decoded hide memory latency; at full streaming rate the loaded latency
-// is several microseconds, which takes several sets per wavefront (an even number: the activation
-// registers alternate by phase parity).
-constexpr int kDepth = 4;
 
 template <int K, int CB, int L, int OT>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
@@ -168,8 +62,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   const uint32_t step_t = 16u * kstride;          // bytes per iteration (4 k-tile rows)
 
   auto issue_it = [&](Stage<K>& st, int it) {
-    // the iteration index is wave-uniform: keep the advancing offset in an SGPR (buffer soffset)
-    load_run<K>(rs_t, vo_t, vo_wp, __builtin_amdgcn_readfirstlane((uint32_t)it * step_t), st.w, st.wp);
+    // the advance goes into the per-lane offset, which the descriptor's range check covers
+    const uint32_t adv = (uint32_t)it * step_t;
+    load_run<K>(rs_t, vo_t + adv, vo_wp + adv, 0u, st.w, st.wp);
   };
 
   Stage<K> st[D];
@@ -299,11 +194,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     if (last == 0) return;
     for (int idx = tid; idx < rows * 128; idx += 256) {
       const int r = idx >> 7, cc = idx & 127;
-      const float* src = part + (size_t)r * a.n_total + blk * 128 + cc;
-      float v = 0.f;
-      for (int ss = 0; ss < a.S; ++ss)
-        v += __hip_atomic_load(src + (size_t)ss * pstride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      bv[r][cc] = v;
+      bv[r][cc] = sum_splits(part + (size_t)r * a.n_total + blk * 128 + cc, pstride, a.S);
     }
     if (tid == 0) __hip_atomic_store(&a.counters[blk], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
@@ -409,7 +300,12 @@ using namespace exl3;
 extern "C" size_t exl3_gemv_workspace_bytes(int k, int n_total, int rows, int K) {
   if (k <= 0 || k % 16 || n_total <= 0 || n_total % 128 || rows < 1 || rows > kMaxRows || K < 1 || K > 8) return 0;
   const int KT = k / 16, blocks = n_total / 128;
-  return workspace_for(KT, blocks, rows, n_total, auto_kt_per_split(KT, blocks));
+  size_t bytes = workspace_for(KT, blocks, rows, n_total, auto_kt_per_split(KT, blocks));
+  if (KT % 4 == 0) {
+    const size_t lut = gemv_lut_workspace(KT, n_total, rows);
+    if (lut > bytes) bytes = lut;
+  }
+  return bytes;
 }
 
 extern "C" int exl3_gemv_ex(const uint16_t* xh, const uint32_t* const* trellis, int n_members, const int* member_n,
@@ -423,7 +319,8 @@ extern "C" int exl3_gemv_ex(const uint16_t* xh, const uint32_t* const* trellis, 
   EXL3_REQUIRE(cb >= 0 && cb <= 2, EXL3_ERR_ARG, "exl3_gemv: codebook must be 0, 1 or 2 (got %d)", cb);
   EXL3_REQUIRE(rows >= 1 && rows <= kMaxRows, EXL3_ERR_ARG, "exl3_gemv: rows must be 1..%d (got %d)", kMaxRows, rows);
   EXL3_REQUIRE(out_dtype >= 0 && out_dtype <= 2, EXL3_ERR_ARG, "exl3_gemv: bad out_dtype %d", out_dtype);
-  EXL3_REQUIRE((flags & ~1u) == 0, EXL3_ERR_ARG, "exl3_gemv: unknown flags 0x%x", flags);
+  EXL3_REQUIRE((flags & ~(EXL3_GEMV_FAST | EXL3_GEMV_TABLE)) == 0, EXL3_ERR_ARG, "exl3_gemv: unknown flags 0x%x",
+               flags);
   EXL3_REQUIRE(aligned(xh, 16), EXL3_ERR_ARG, "exl3_gemv: xh must be 16-byte aligned");
   GemvArgs a{};
   int n_total = 0;
@@ -444,6 +341,41 @@ extern "C" int exl3_gemv_ex(const uint16_t* xh, const uint32_t* const* trellis, 
     a.blk_end[i] = 1 << 30;
   }
   const int KT = k / 16, blocks = n_total / 128;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  bool table_ok = kt_per_split <= 0 && (flags & EXL3_GEMV_TABLE) && gemv_lut_eligible(k, K, cb, flags);
+  for (int i = 0; i < n_members && table_ok; ++i) table_ok = gemv_lut_offsets_fit(k, member_n[i], K);
+  if (table_ok) {
+    GemvLutArgs b{};
+    for (int i = 0; i < 3; ++i) {
+      b.tr[i] = a.tr[i];
+      b.NT[i] = a.NT[i];
+      b.cg_end[i] = a.blk_end[i] == (1 << 30) ? (1 << 30) : a.blk_end[i] * 4;
+    }
+    int S = 1, kps = 4;
+    gemv_lut_split(KT, n_total, &S, &kps);
+    const size_t need = gemv_lut_workspace(KT, n_total, rows);
+    EXL3_REQUIRE(workspace && workspace_bytes >= need && aligned(workspace, 256), EXL3_ERR_WORKSPACE,
+                 "exl3_gemv: a zero-initialised, 256-byte aligned workspace of %zu bytes is needed (got %zu)", need,
+                 workspace_bytes);
+    b.xh = xh;
+    b.svh = svh;
+    b.bias = bias;
+    b.y = y;
+    b.counters = static_cast<uint32_t*>(workspace);
+    b.partials = reinterpret_cast<float*>(static_cast<char*>(workspace) + counters_bytes(blocks));
+    b.k = k;
+    b.KT = KT;
+    b.rows = rows;
+    b.n_total = n_total;
+    b.S = S;
+    b.kt_per_split = kps;
+    b.n_cg = n_total / 32;
+    b.n_pieces = b.n_cg * S;
+    const int rc = gemv_lut_launch(b, K, cb, out_dtype, st);
+    if (rc != EXL3_OK) return rc;
+    EXL3_LAUNCH_CHECK("exl3_gemv");
+    return EXL3_OK;
+  }
   const int layout = layout_for(cb, flags);
   const int kps = kt_per_split > 0 ? ((kt_per_split + 3) / 4) * 4 : auto_kt_per_split(KT, blocks);
   // staged activations: ((iters + 1) * 4 * rows + 1) records of 32 bytes
@@ -466,7 +398,6 @@ extern "C" int exl3_gemv_ex(const uint16_t* xh, const uint32_t* const* trellis, 
   a.n_total = n_total;
   a.S = S;
   a.kt_per_split = kps;
-  hipStream_t st = static_cast<hipStream_t>(stream);
   switch (K) {
     case 1: dispatch_cb<1>(cb, layout, out_dtype, a, blocks, smem, st); break;
     case 2: dispatch_cb<2>(cb, layout, out_dtype, a, blocks, smem, st); break;

@@ -1,0 +1,183 @@
+// SPDX-License-Identifier: Apache-2.0
+// Device helpers shared by the two EXL3 GEMV kernels (exl3_gemv.hip: one workgroup per 128-column block and
+// k-split; exl3_gemv_lut.hip: persistent workgroups with an LDS codebook table), and the interface between the
+// entry point and the table kernel's launcher.
+#pragma once
+
+#include "exl3_capi_common.h"
+#include "exl3_device.h"
+
+namespace exl3 {
+
+struct GemvArgs {
+  const uint16_t* xh;
+  const uint32_t* tr[3];
+  int NT[3];
+  int blk_end[3];
+  const uint16_t* svh;
+  const void* bias;
+  void* y;
+  float* partials;
+  uint32_t* counters;
+  int k, KT, rows, n_total, S, kt_per_split;
+};
+
+constexpr int kMaxRows = 16;
+constexpr int kBufferFlags = 0x00020000;   // raw buffer descriptor word 3 (32-bit data, no swizzle) for gfx950
+
+__device__ __forceinline__ uint32_t bitop_split(uint32_t h, uint32_t mask_s, uint32_t xor_v) {
+  uint32_t u;
+  asm("v_bitop3_b32 %0, %1, %2, %3 bitop3:0x6a" : "=v"(u) : "v"(h), "s"(mask_s), "v"(xor_v));   // (h & M) ^ X
+  return u;
+}
+
+// Decode one run (32 positions) of K words + the word before into MFMA B registers.
+//   SPLIT: b[p] = (a_p, b_p) fp16 summands, p = 0..31
+//   pair : b[p/2] = (w_p, w_{p+1}) fp16, p even, 16 registers
+template <int K, int CB, bool SPLIT>
+__device__ __forceinline__ void decode_run(const uint32_t* w, uint32_t wp, uint32_t* b, uint32_t xor_v) {
+  if constexpr (SPLIT) {
+    static_for<0, 32>([&](auto P) {
+      constexpr int p = decltype(P)::value;
+      b[p] = bitop_split(hash_pos<CB, K, p>(w, wp), kMask3, xor_v);
+    });
+  } else if constexpr (CB == 2) {
+    static_for<0, 16>([&](auto P) {
+      constexpr int p = 2 * decltype(P)::value;
+      b[p / 2] = mul1_pair(mul1_r(hash_pos<CB, K, p>(w, wp)), mul1_r(hash_pos<CB, K, p + 1>(w, wp)));
+    });
+  } else {
+    static_for<0, 16>([&](auto P) {
+      constexpr int p = 2 * decltype(P)::value;
+      b[p / 2] = sum_pairs(bitop_split(hash_pos<CB, K, p>(w, wp), kMask3, xor_v),
+                           bitop_split(hash_pos<CB, K, p + 1>(w, wp), kMask3, xor_v));
+    });
+  }
+}
+
+// Buffer loads of a run's K stream words (at byte offset vo) and the word before the run (at vo_wp), both
+// plus the scalar offset soff (callers pass 0 and put any advance in vo / vo_wp, which the descriptor's range
+// check covers). The buffer descriptor ends at the end of the k-split, so
+// prefetches past the split return zeros without touching memory.
+template <int K>
+__device__ __forceinline__ void load_run(__amdgpu_buffer_rsrc_t rs, uint32_t vo, uint32_t vo_wp, uint32_t soff,
+                                         uint32_t* w, uint32_t& wp) {
+  int i = 0;
+#pragma unroll
+  for (; i + 4 <= K; i += 4) {
+    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, vo + 4 * i, soff, 0);
+    w[i] = v.x; w[i + 1] = v.y; w[i + 2] = v.z; w[i + 3] = v.w;
+  }
+  if constexpr (K % 4 == 3) {
+    const u32x3 v = __builtin_amdgcn_raw_buffer_load_b96(rs, vo + 4 * (K - 3), soff, 0);
+    w[K - 3] = v.x; w[K - 2] = v.y; w[K - 1] = v.z;
+  } else if constexpr (K % 4 == 2) {
+    const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rs, vo + 4 * (K - 2), soff, 0);
+    w[K - 2] = v.x; w[K - 1] = v.y;
+  } else if constexpr (K % 4 == 1) {
+    w[K - 1] = __builtin_amdgcn_raw_buffer_load_b32(rs, vo + 4 * (K - 1), soff, 0);
+  }
+  wp = __builtin_amdgcn_raw_buffer_load_b32(rs, vo_wp, soff, 0);
+}
+
+template <typename T>
+__device__ __forceinline__ f16x8 as_f16x8(const T& v) { return __builtin_bit_cast(f16x8, v); }
+
+// The B operands are produced by inline asm, which the compiler's hazard tracking does not count as VALU
+// writes, so it would not insert the wait states an MFMA needs after a VALU write of its source VGPRs.
+// This barrier re-defines the four registers after two wait states (s_nop 1): the MFMA then reads values
+// whose last real writer is at least two instructions back, and the data dependence keeps the decode asm
+// from being scheduled past it.
+__device__ __forceinline__ u32x4 mfma_src(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  asm volatile("s_nop 1" : "+v"(a), "+v"(b), "+v"(c), "+v"(d));
+  return u32x4{a, b, c, d};
+}
+
+// Activation (A operand) layouts of the kernel:
+//   kPair   B registers hold two fp16-rounded codebook values (k pair); A = xh's natural fp16 pairs
+//   kSplit  B registers hold the two fp16 summands of one value; A = each activation twice, built from the
+//           natural pairs with byte permutes (2 instructions per k pair)
+enum Layout : int { kPair = 0, kSplit = 1 };
+
+// One trellis prefetch set of a lane: its run's K stream words and the word before the run.
+template <int K>
+struct Stage {
+  uint32_t w[K];
+  uint32_t wp;
+};
+
+__device__ __forceinline__ u32x4 dup4(uint32_t d0, uint32_t d1) {   // (x0,x1),(x2,x3) -> x0 x0, x1 x1, x2 x2, x3 x3
+  return u32x4{__builtin_amdgcn_perm(d0, d0, 0x01000100u), __builtin_amdgcn_perm(d0, d0, 0x03020302u),
+               __builtin_amdgcn_perm(d1, d1, 0x01000100u), __builtin_amdgcn_perm(d1, d1, 0x03020302u)};
+}
+
+// Trellis sets in flight per lane. Decoding keeps the VALU busy for ~1 us per set per SIMD, so only the
+// sets queued behind the one being decoded hide memory latency; at full streaming rate the loaded latency
+// is several microseconds, which takes several sets per wavefront (an even number: the activation
+// registers alternate by phase parity).
+constexpr int kDepth = 4;
+
+
+// Sum of S split partials src[0], src[stride], ..., in split order, read with device-scope loads. The loads
+// are issued eight at a time before any is used, so the sum costs ceil(S / 8) memory round trips, not S.
+__device__ __forceinline__ float sum_splits(const float* src, size_t stride, int S) {
+  float v = 0.f;
+  for (int s0 = 0; s0 < S; s0 += 8) {
+    float t[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      t[u] = s0 + u < S ? __hip_atomic_load(src + (size_t)(s0 + u) * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                        : 0.f;
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (s0 + u < S) v += t[u];
+  }
+  return v;
+}
+
+// Two adjacent columns of S split partials (src[s * stride], src[s * stride + 1]), as sum_splits.
+__device__ __forceinline__ void sum_splits2(const float* src, size_t stride, int S, float& v0, float& v1) {
+  v0 = 0.f;
+  v1 = 0.f;
+  for (int s0 = 0; s0 < S; s0 += 8) {
+    float t0[8], t1[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const bool ok = s0 + u < S;
+      const float* p = src + (size_t)(ok ? s0 + u : 0) * stride;
+      t0[u] = ok ? __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
+      t1[u] = ok ? __hip_atomic_load(p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (s0 + u < S) {
+        v0 += t0[u];
+        v1 += t1[u];
+      }
+  }
+}
+
+// ---- table GEMV (exl3_gemv_lut.hip) ----
+struct GemvLutArgs {
+  const uint16_t* xh;        // (n_members, rows, k) fp16
+  const uint32_t* tr[3];
+  int NT[3];                 // n-tiles per member
+  int cg_end[3];             // cumulative 32-column groups per member
+  const uint16_t* svh;
+  const void* bias;
+  void* y;
+  float* partials;           // S x rows x n_total
+  uint32_t* counters;        // one per 128-column block
+  const uint16_t* lut;       // the codebook's table in device memory
+  int k, KT, rows, n_total, S, kt_per_split, n_cg, n_pieces;
+};
+
+// Split of the table GEMV: pieces = (32-column group, k-split), about 4096 of them (16 per CU on 256 CUs),
+// each a whole number of 4-k-tile steps. Depends on the shape only (row-exact results).
+void gemv_lut_split(int KT, int n_total, int* S, int* kt_per_split);
+size_t gemv_lut_workspace(int KT, int n_total, int rows);
+bool gemv_lut_eligible(int k, int K, int cb, unsigned flags);
+bool gemv_lut_offsets_fit(int k, int n, int K);
+int gemv_lut_launch(GemvLutArgs& a, int K, int cb, int out_dtype, hipStream_t st);
+
+}  // namespace exl3

@@ -109,7 +109,15 @@ extern "C" const char* exl3_last_error(void) { return g_error; }
 extern "C" int exl3_codebook(int cb, int hi_half, uint16_t* out, void* stream) {
   EXL3_REQUIRE(cb >= 0 && cb <= 2, EXL3_ERR_ARG, "exl3_codebook: codebook must be 0, 1 or 2 (got %d)", cb);
   EXL3_REQUIRE(out != nullptr, EXL3_ERR_ARG, "exl3_codebook: out is NULL");
+  EXL3_REQUIRE(hi_half >= 0 && hi_half <= 2, EXL3_ERR_ARG, "exl3_codebook: hi_half must be 0, 1 or 2");
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (hi_half == 2) {
+    const uint16_t* table = codebook_table(cb);
+    EXL3_REQUIRE(table != nullptr, EXL3_ERR_HIP, "exl3_codebook: table %d unavailable on this device", cb);
+    const hipError_t e = hipMemcpyAsync(out, table, 65536 * sizeof(uint16_t), hipMemcpyDeviceToDevice, st);
+    EXL3_REQUIRE(e == hipSuccess, EXL3_ERR_HIP, "exl3_codebook: copy failed: %s", hipGetErrorString(e));
+    return EXL3_OK;
+  }
   const unsigned blocks = 32768 / 256;
   if (hi_half) {
     if (cb == 0) codebook_kernel<0, true><<<blocks, 256, 0, st>>>(out);

@@ -18,7 +18,7 @@ from ._capi import DTYPE_CODE, Exl3Error, check, lib, ptr, stream_handle
 
 MAX_GEMV_ROWS = 8           # rows at or below which EXL3Linear takes the GEMV path (kernels.py:260)
 GEMV_ROWS_LIMIT = 16        # rows one GEMV launch accepts
-GEMV_EXACT, GEMV_FAST = 0, 1
+GEMV_EXACT, GEMV_FAST, GEMV_TABLE = 0, 1, 2
 
 
 def _require(cond: bool, msg: str) -> None:
@@ -39,10 +39,12 @@ def trellis_words(trellis: torch.Tensor, k: int, n: int, K: int) -> torch.Tensor
     return trellis
 
 
-def codebook(cb: int, hi_half: bool = False, device=None) -> torch.Tensor:
-    """All 65,536 codebook values (fp16) through the kernels' decode path."""
+def codebook(cb: int, hi_half: bool = False, device=None, table: bool = False) -> torch.Tensor:
+    """All 65,536 codebook values (fp16) through the kernels' hashing decoder (state from the low or high
+    half of a word), or the lookup table the table GEMV kernel uses (table=True)."""
     out = torch.empty(65536, dtype=torch.float16, device=device or "cuda")
-    check(lib().exl3_codebook(cb, int(hi_half), ptr(out), stream_handle(out.device)), "exl3_codebook")
+    src = 2 if table else int(hi_half)
+    check(lib().exl3_codebook(cb, src, ptr(out), stream_handle(out.device)), "exl3_codebook")
     return out
 
 
@@ -125,10 +127,14 @@ class TrellisGemvPlan:
     """y = had128(xh @ W_inner) * svh (+ bias) in out_dtype for one EXL3 linear or a sibling group of
     <= 3 members sharing K and codebook (kernels.py:263-299). xh is (n_members, rows, k): each member's own
     rotated input. The plan owns the launch parameters and a zeroed workspace (split-K partials and
-    per-block arrival counters that the kernel leaves at zero)."""
+    per-block arrival counters that the kernel leaves at zero).
+
+    Kernels: the hashing kernel by default; table=True selects the table kernel (LDS codebook lookup for
+    half of each run) for exact contraction when k % 64 == 0. kt_per_split is a hashing-kernel knob."""
 
     def __init__(self, k: int, member_ns: list[int], K: int, cb: int, svh: torch.Tensor, rows: int,
-                 out_dtype: torch.dtype = torch.float16, *, fast: bool = False, kt_per_split: int = 0):
+                 out_dtype: torch.dtype = torch.float16, *, fast: bool = False, kt_per_split: int = 0,
+                 table: bool = False):
         _require(k % 16 == 0 and all(n % 128 == 0 for n in member_ns) and 1 <= K <= 8 and cb in (0, 1, 2),
                  "TrellisGemvPlan: k % 16, n % 128, 1 <= K <= 8, codebook 0..2")
         _require(1 <= len(member_ns) <= 3 and 1 <= rows <= GEMV_ROWS_LIMIT, "TrellisGemvPlan: 1..3 members, rows")
@@ -136,7 +142,7 @@ class TrellisGemvPlan:
         self.k, self.ns, self.n, self.K, self.cb, self.rows = k, list(member_ns), sum(member_ns), K, cb, rows
         self.out_dtype = out_dtype
         self.nsub = len(member_ns)
-        self.flags = GEMV_FAST if fast else GEMV_EXACT
+        self.flags = (GEMV_FAST if fast else GEMV_EXACT) | (GEMV_TABLE if table else 0)
         self.kt_per_split = kt_per_split
         self.svh = svh.to(torch.float16).reshape(-1).contiguous()
         _require(self.svh.numel() == self.n, "TrellisGemvPlan: svh must have sum(member_ns) elements")

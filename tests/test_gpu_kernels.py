@@ -326,3 +326,37 @@ def test_attn_decode_out_of_range_position_writes_nothing(pk):
         xh, o = pk.kernels.attn_decode_rotate(z(nh * hd), z(nkv * hd), z(nkv * hd), kc, vc, p, cos, sin,
                                               z(nh * hd), want_o=True)
         assert (o == 0).all() and (xh == 0).all() and (kc == 1).all() and (vc == 1).all()
+
+
+# ------------------------------------------------------------------------------------------ table kernel
+@pytest.mark.parametrize("cb", [0, 1, 2])
+def test_codebook_table_matches_decoder_and_oracle(pk, cb):
+    """The compile-time lookup table == the hashing decoder (both halves) == the oracle, all 65,536 states."""
+    t = pk.kernels.codebook(cb, table=True)
+    assert torch.equal(t, pk.kernels.codebook(cb)) and torch.equal(t, pk.kernels.codebook(cb, hi_half=True))
+    assert np.array_equal(f16_bits(t), O.codebook_table(cb))
+
+
+@pytest.mark.parametrize("K", range(1, 9))
+@pytest.mark.parametrize("cb", [0, 1, 2])
+def test_gemv_table_kernel_vs_hash_kernel(pk, K, cb):
+    """Table kernel (exact contraction, k % 64 == 0) against the hashing kernel and the oracle, one to three
+    members, rows 1 / 5 / 16, fp32 output; and row-exact (row 0 identical for 1 and 16 rows)."""
+    k, ns = 1024, [256, 128, 384][: 1 + (K % 3)]
+    rng = np.random.default_rng(K * 10 + cb)
+    trs = [O.random_trellis(k, n, K, K * 100 + cb * 10 + i) for i, n in enumerate(ns)]
+    svh = (rng.standard_normal(sum(ns)) * 0.01).astype(np.float16)
+    ws = [O.reconstruct_inner(t, k, n, K, cb) for t, n in zip(trs, ns)]
+    offs = np.cumsum([0] + list(ns))
+    for rows in (1, 5, 16):
+        xh = rng.standard_normal((len(ns), rows, k)).astype(np.float16)
+        ref = np.concatenate([O.gemv_ref(xh[m], ws[m], svh[offs[m]:offs[m + 1]]) for m in range(len(ns))], axis=1)
+        ys = []
+        for table in (True, False):
+            plan = pk.kernels.TrellisGemvPlan(k, ns, K, cb, dev(svh), rows, torch.float32, table=table)
+            ys.append(plan(dev(xh), [dev(t) for t in trs]))
+            assert O.max_abs_rel(ys[-1].cpu().numpy(), ref) < 2e-3, (K, cb, rows, table)
+        assert O.max_abs_rel(ys[0].cpu().numpy(), ys[1].cpu().numpy()) < 1e-4
+        if rows == 16:
+            plan1 = pk.kernels.TrellisGemvPlan(k, ns, K, cb, dev(svh), 1, torch.float32, table=True)
+            assert torch.equal(plan1(dev(xh[:, :1].copy()), [dev(t) for t in trs])[0], ys[0][0])
