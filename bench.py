@@ -15,6 +15,8 @@ Inputs (rotated activations, trellis, svh) are resident in HBM before timing sta
                  HIP events on the launch stream, against the 8 TB/s HBM3E peak; traffic = HBM bytes per
                  launch from rocprofv3 FETCH_SIZE / WRITE_SIZE (profiles/), or null
   cpu_baseline   the NumPy oracle (reconstruct + fp32 matmul + Hadamard + svh) on the q projection
+  mixed_k        config 3: the 27B projections with K drawn per tensor from {2,3,4,5,6,8}, rows 1 / 2 / 4 / 8
+  prefill        config 4: M = 4608 through gate / up / down at K = 6, TFLOP/s against the fp16 MFMA peak
   decode_tok_s   end-to-end batch-1 greedy decode of the synthetic 27B-shape EXL3 decoder (config 5: 64
                  layers, hidden 5120, MLP 17408, GQA 48/8 x 128, head 5120 -> 151936, K = 6): a 512-token
                  random-id prompt, then 256 tokens, each decode step replayed from one captured HIP graph
@@ -127,6 +129,96 @@ def cpu_baseline(seconds_budget: float = 30.0) -> dict:
     }
 
 
+MFMA_F16_PEAK_TFLOPS = 2500.0
+# 27B projections as separate tensors (a mixed-bitrate checkpoint groups only siblings of equal K)
+PROJ = [("q", 5120, 6144), ("k", 5120, 1024), ("v", 5120, 1024), ("o", 6144, 5120), ("gate", 5120, 17408),
+        ("up", 5120, 17408), ("down", 17408, 5120)]
+
+
+def mixed_k_benchmark(pk, torch, dev, rows_list=(1, 2, 4, 8), n_layers=8, reps=4) -> dict:
+    """Config 3: the 27B projections with K drawn per tensor from {2, 3, 4, 5, 6, 8} (seeded), siblings of
+    equal K grouped as the loader groups them, at batch rows 1, 2, 4, 8. Layers rotate over a working set
+    beyond the Infinity Cache; GB/s = algorithmic bytes (at the drawn K) / time, launches timed back to back."""
+    import random
+    rnd = random.Random(3)
+    g = torch.Generator(device=dev).manual_seed(77)
+    layers, draws = [], []
+    for _ in range(n_layers):
+        Ks = {name: rnd.choice([2, 3, 4, 5, 6, 8]) for name, _, _ in PROJ}
+        draws.append(Ks)
+        groups = []
+        for sib in (("q", "k", "v"), ("gate", "up"), ("o",), ("down",)):
+            by_k = {}
+            for name in sib:
+                by_k.setdefault(Ks[name], []).append(name)
+            for K, names in by_k.items():
+                k = [p[1] for p in PROJ if p[0] == names[0]][0]
+                ns = [[p[2] for p in PROJ if p[0] == nm][0] for nm in names]
+                trs = [torch.randint(-32768, 32768, (k // 16, n // 16, 16 * K), dtype=torch.int16, device=dev,
+                                     generator=g) for n in ns]
+                svh = torch.where(torch.rand(sum(ns), device=dev, generator=g) < 0.5, -1.0, 1.0).half()
+                groups.append((k, ns, K, trs, svh))
+        layers.append(groups)
+    out = {"draws": draws, "per_rows": {}}
+    bpw = sum(K * k * n for Ks in draws for (name, k, n) in PROJ for K in [Ks[name]]) / \
+        sum(k * n for _ in draws for (_, k, n) in PROJ)
+    out["mean_bpw"] = round(bpw, 3)
+    for rows in rows_list:
+        items, nbytes = [], 0
+        for groups in layers:
+            for k, ns, K, trs, svh in groups:
+                plan = pk.kernels.TrellisGemvPlan(k, ns, K, 0, svh, rows, torch.float16)
+                xh = torch.randn((len(ns), rows, k), device=dev, generator=g).half()
+                o = torch.empty((rows, sum(ns)), dtype=torch.float16, device=dev)
+                items.append((plan, xh, trs, o))
+                nbytes += algorithmic_bytes(k, ns, K, rows)
+        for plan, xh, trs, o in items:
+            plan(xh, trs, out=o)
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(reps):
+            for plan, xh, trs, o in items:
+                plan(xh, trs, out=o)
+        e.record()
+        torch.cuda.synchronize()
+        ms = s.elapsed_time(e) / reps
+        out["per_rows"][str(rows)] = {"us_per_layer": round(ms * 1e3 / n_layers, 1),
+                                      "GB_s": round(nbytes / ms / 1e6, 1),
+                                      "pct_hbm_peak": round(100 * nbytes / ms / 1e6 / HBM_PEAK_GBS, 1)}
+    return out
+
+
+def prefill_benchmark(pk, torch, dev, rows=4608, reps=3) -> dict:
+    """Config 4: M = 4608 rotated fp16 activations through gate / up (5120 -> 17408) and down (17408 -> 5120)
+    at K = 6, each one fused launch (trellis tiles reconstructed in LDS, MFMA, Hadamard epilogue).
+    TFLOP/s = 2 M k n / time, against the 2.5 PFLOP/s dense fp16 MFMA peak."""
+    g = torch.Generator(device=dev).manual_seed(5)
+    res, tot_flop, tot_ms = {}, 0.0, 0.0
+    for name, k, n in (("gate", 5120, 17408), ("up", 5120, 17408), ("down", 17408, 5120)):
+        tr = torch.randint(-32768, 32768, (k // 16, n // 16, 96), dtype=torch.int16, device=dev, generator=g)
+        svh = torch.where(torch.rand(n, device=dev, generator=g) < 0.5, -1.0, 1.0).half()
+        xh = torch.randn((rows, k), device=dev, generator=g).half()
+        out = torch.empty((rows, n), dtype=torch.float16, device=dev)
+        pk.kernels.prefill_gemm(xh, tr, k, n, 6, 0, svh, out=out)
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(reps):
+            pk.kernels.prefill_gemm(xh, tr, k, n, 6, 0, svh, out=out)
+        e.record()
+        torch.cuda.synchronize()
+        ms = s.elapsed_time(e) / reps
+        flop = 2.0 * rows * k * n
+        res[name] = {"ms": round(ms, 3), "TFLOP_s": round(flop / ms / 1e9, 1)}
+        tot_flop += flop
+        tot_ms += ms
+        del tr, xh, out
+    tf = tot_flop / tot_ms / 1e9
+    return {"rows": rows, "per_proj": res, "TFLOP_s": round(tf, 1), "peak_TFLOP_s": MFMA_F16_PEAK_TFLOPS,
+            "mfma_frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4), "ms_total": round(tot_ms, 2)}
+
+
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -202,6 +294,7 @@ def main() -> int:
                     help="run only a 1 GiB device copy (calibrates rocprofv3 FETCH/WRITE counters)")
     ap.add_argument("--decoder-layers", type=int, default=64, help="layers of the end-to-end decoder (0 = skip)")
     ap.add_argument("--prompt", type=int, default=512)
+    ap.add_argument("--no-configs", action="store_true", help="skip the mixed-K (config 3) and prefill (config 4) lines")
     ap.add_argument("--gen", type=int, default=256)
     args = ap.parse_args()
 
@@ -349,6 +442,13 @@ def main() -> int:
     del layers, evs, graph
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
+    if not args.no_configs:
+        result["mixed_k"] = mixed_k_benchmark(pk, torch, dev)
+        log(f"mixed K: {result['mixed_k']['per_rows']}")
+        torch.cuda.empty_cache()
+        result["prefill"] = prefill_benchmark(pk, torch, dev)
+        log(f"prefill: {result['prefill']['TFLOP_s']} TFLOP/s")
+        torch.cuda.empty_cache()
     if args.decoder_layers > 0:
         dec = decode_benchmark(pk, torch, dev, args.decoder_layers, args.prompt, args.gen)
         result["decode_tok_s"] = dec["tok_s"]
