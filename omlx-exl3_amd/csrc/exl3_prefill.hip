@@ -2,141 +2,207 @@
 // Prefill contraction for EXL3 linears on gfx950: y = had128(xh @ W_inner) * svh (+ bias) for many rows
 // (replaces EXL3Linear._prefill, reference src/omlx/exl3/linear.py:97-105: decode_wt to HBM + MLX matmul
 // + hadamard_transform + svh). The weights never exist in HBM as fp16: each workgroup reconstructs the
-// trellis tiles of its k-step into LDS (bit-exact fp16, the reconstruct kernel's decode) and contracts
-// them on MFMA with fp32 accumulation; the 128-column output tile is one Hadamard block, so the output
-// rotation, svh and bias are applied in the epilogue.
+// trellis tiles of its k-step into LDS (bit-exact fp16 pairs, the GEMV's decoder) and contracts them on MFMA
+// with fp32 accumulation; the 128-column output tile is one Hadamard block, so the output rotation, svh and
+// bias are applied in the epilogue.
 //
-// Tiling: workgroup = 256 threads (4 wavefronts) computes a BM x 128 tile; k advances 64 at a time
-// (4 k-tiles x 8 n-tiles = 32 trellis tiles = 256 runs, one run per thread). Wavefront w owns rows
-// [w*BM/4, (w+1)*BM/4) of the tile and all 128 columns.
+// Workgroup = 512 threads, tile = 256 rows x 128 columns, k advances 64 per step, in two roles:
+//   decode wavefronts (4-7): one trellis run per lane per step (4 k-tiles x 8 n-tiles x 8 runs = 256 runs),
+//     prefetched two steps ahead, decoded into the next step's half of a double-buffered LDS weight tile
+//     (n-major, 16-byte pair groups, the B-operand layout of v_mfma_f32_16x16x32_f16);
+//   MFMA wavefronts (0-3): 64 rows each; activations loaded straight into A-operand registers one 32-k
+//     slice ahead (rows past the batch read zero through the buffer descriptor), 64 MFMAs per step against
+//     the current half of the weight tile.
+// One barrier per step hands the tile halves over, so decoding (VALU) overlaps the matrix work (MFMA) on
+// the same SIMDs. Epilogue: the 128-point FWHT of each row runs in registers (stages 1, 2, 4, 8 across the 16
+// lanes of a column group, 16, 32, 64 across the accumulator tiles of a lane), then 1/sqrt(128), svh, bias.
 #include "exl3_capi_common.h"
 #include "exl3_device.h"
+#include "exl3_gemv_common.h"
 
 namespace exl3 {
 
-constexpr int kPfBM = 128;          // rows per workgroup tile
+constexpr int kPfBM = 256;          // rows per workgroup tile
 constexpr int kPfBK = 64;           // k per step
-constexpr int kPfRowsW = kPfBM / 4; // rows per wavefront (32 = 2 MFMA row tiles)
-constexpr int kPfLdA = kPfBK + 8;   // padded LDS row pitch (halves) of the activation tile
 constexpr int kPfLdB = kPfBK + 8;   // padded LDS row pitch (halves) of the weight tile (n-major)
+constexpr int kPfThreads = 512;
 
 template <int K, int CB, int OT>
-__global__ __launch_bounds__(256) void prefill_kernel(const uint16_t* __restrict__ xh, const uint32_t* __restrict__ tr,
-                                                      int k, int n, int rows, const uint16_t* __restrict__ svh,
-                                                      const void* __restrict__ bias, void* __restrict__ y) {
+__global__ __launch_bounds__(kPfThreads) void prefill_kernel(const uint16_t* __restrict__ xh,
+                                                             const uint32_t* __restrict__ tr, int k, int n, int rows,
+                                                             const uint16_t* __restrict__ svh,
+                                                             const void* __restrict__ bias, void* __restrict__ y) {
   constexpr int TW = 8 * K;
-  __shared__ __attribute__((aligned(16))) uint16_t sA[kPfBM * kPfLdA];
-  __shared__ __attribute__((aligned(16))) uint16_t sB[128 * kPfLdB];
-  __shared__ float sC[4][32][129];
+  __shared__ __attribute__((aligned(16))) uint16_t sB[2][128 * kPfLdB];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int nb = blockIdx.x;                 // 128-column block
-  const int mb = blockIdx.y;                 // BM-row block
+  const int row0 = blockIdx.y * kPfBM;
   const int KT = k / 16, NT = n / 16;
-  const int row0 = mb * kPfBM;
+  const int nsteps = (KT + 3) / 4;
+  const bool decoder = wave >= 4;
 
-  // this thread's run in each k-step: k-tile (tid >> 6) of the step, n-tile ((tid >> 3) & 7), run g
-  const int r_kt = tid >> 6, r_nt = (tid >> 3) & 7, r_g = tid & 7;
-
-  f32x4 acc[2][8];
+  // ---------------- decode role ----------------
+  // lane's run in each step: k-tile (t >> 6) of the step, n-tile ((t >> 3) & 7), run g = t & 7
+  const int t = tid & 255;
+  const int r_kt = t >> 6, r_nt = (t >> 3) & 7, r_g = t & 7;
+  const uint32_t* trun = tr + ((size_t)r_kt * NT + nb * 8 + r_nt) * TW;   // + step * 4 * NT * TW
+  const size_t tstep = (size_t)4 * NT * TW;
+  const int wofs = K * r_g, wpofs = (K * r_g + TW - 1) % TW;
+  auto load_run_words = [&](int s, uint32_t* w, uint32_t& wp) {
+    if (s < nsteps && s * 4 + r_kt < KT) {
+      const uint32_t* tp = trun + (size_t)s * tstep;
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < K; ++i) w[i] = tp[wofs + i];
+      wp = tp[wpofs];
+    } else {
+#pragma unroll
+      for (int i = 0; i < K; ++i) w[i] = 0u;
+      wp = 0u;
+    }
+  };
+  // decoded run -> LDS: column g (lo) and 8 + g (hi) of n-tile r_nt, k 16 r_kt .. 16 r_kt + 15
+  auto store_run = [&](int buf, int s, const uint32_t* w, uint32_t wp) {
+    uint32_t b[16];
+    if (s * 4 + r_kt < KT) {
+      decode_run<K, CB, false>(w, wp, b, kXor3);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) b[i] = 0u;   // k past the matrix: zero weights
+    }
+    uint16_t* blo = sB[buf] + (r_nt * 16 + r_g) * kPfLdB + r_kt * 16;
+    uint16_t* bhi = sB[buf] + (r_nt * 16 + 8 + r_g) * kPfLdB + r_kt * 16;
+    // b[i] holds positions 2i, 2i+1; k pairs of the lo column: (0,1) b0 (2,3) b4 (4,5) b8 (6,7) b12,
+    // (8,9) b1 .. (14,15) b13; the hi column: b2 b6 b10 b14, b3 b7 b11 b15
+    reinterpret_cast<u32x4*>(blo)[0] = u32x4{b[0], b[4], b[8], b[12]};
+    reinterpret_cast<u32x4*>(blo)[1] = u32x4{b[1], b[5], b[9], b[13]};
+    reinterpret_cast<u32x4*>(bhi)[0] = u32x4{b[2], b[6], b[10], b[14]};
+    reinterpret_cast<u32x4*>(bhi)[1] = u32x4{b[3], b[7], b[11], b[15]};
+  };
+
+  // ---------------- MFMA role ----------------
+  // lane (16q + c): A rows 16 i + c of this wavefront's 64, k 8q .. 8q+7 of each 32-k slice
+  const int q = lane >> 4, c = lane & 15;
+  const int wrow0 = row0 + wave * 64;
+  const __amdgpu_buffer_rsrc_t rs_x = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(xh), (short)0, (int)((uint32_t)rows * (uint32_t)k * 2u), kBufferFlags);
+  // A fragments of 32-k slice `g` (= step g / 2, half g % 2) for the 4 row tiles
+  auto load_A = [&](int g, u32x4 (&A)[4]) {
+    const int kk = g * 32 + 8 * q;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = wrow0 + 16 * i + c;
+      // rows past the batch lie past the descriptor (zero); k past the row is zeroed explicitly
+      const uint32_t off = (uint32_t)(r < rows ? r : rows) * (uint32_t)k * 2u + (uint32_t)kk * 2u;
+      u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs_x, off, 0u, 0);
+      if (kk >= k) v = u32x4{0u, 0u, 0u, 0u};
+      A[i] = v;
+    }
+  };
+
+  f32x4 acc[4][8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int k0 = 0; k0 < k; k0 += kPfBK) {
-    // ---- activations: BM rows x 64 k, 16 bytes per thread-iteration ----
-    for (int idx = tid; idx < kPfBM * (kPfBK / 8); idx += 256) {
-      const int r = idx / (kPfBK / 8), c8 = idx % (kPfBK / 8);
-      const int gr = row0 + r, gk = k0 + c8 * 8;
-      u32x4 v = {0u, 0u, 0u, 0u};
-      if (gr < rows && gk < k) v = *reinterpret_cast<const u32x4*>(xh + (size_t)gr * k + gk);
-      *reinterpret_cast<u32x4*>(sA + r * kPfLdA + c8 * 8) = v;
-    }
-    // ---- weights: decode one run per thread into the n-major tile sB[n][k] ----
-    {
-      const int kt = k0 / 16 + r_kt;
-      uint32_t lo[8] = {}, hi[8] = {};
-      if (kt < KT) {
-        const uint32_t* tp = tr + ((size_t)kt * NT + nb * 8 + r_nt) * TW;
-        uint32_t wv[K];
+  // ---------------- pipeline ----------------
+  uint32_t w0[K], w1[K], wp0 = 0, wp1 = 0;   // decode: words of steps s+1 (w0) and s+2 (w1)
+  u32x4 Acur[4], Anext[4];
+  if (decoder) {
+    uint32_t w[K], wp;
+    load_run_words(0, w, wp);
+    load_run_words(1, w0, wp0);
+    load_run_words(2, w1, wp1);
+    store_run(0, 0, w, wp);
+  } else {
+    load_A(0, Acur);
+  }
+  __syncthreads();
+  const int nslices = 2 * nsteps;
+
+  for (int s = 0; s < nsteps; ++s) {
+    if (decoder) {
+      if (s + 1 < nsteps) {
+        uint32_t w[K], wp;
 #pragma unroll
-        for (int i = 0; i < K; ++i) wv[i] = tp[K * r_g + i];
-        const uint32_t wp = tp[(K * r_g + TW - 1) % TW];
-        static_for<0, 32>([&](auto P) {
-          constexpr int p = decltype(P)::value;
-          using W = Win<K, p>;
-          const uint16_t v = dec_one<CB>(hash_pos<CB, K, p>(wv, wp));
-          uint32_t* dst = W::hi_col ? hi : lo;
-          dst[W::k_in >> 1] |= (uint32_t)v << (16 * (W::k_in & 1));
-        });
+        for (int i = 0; i < K; ++i) w[i] = w0[i];
+        wp = wp0;
+#pragma unroll
+        for (int i = 0; i < K; ++i) w0[i] = w1[i];
+        wp0 = wp1;
+        load_run_words(s + 3, w1, wp1);
+        store_run((s + 1) & 1, s + 1, w, wp);
       }
-      uint16_t* blo = sB + (r_nt * 16 + r_g) * kPfLdB + r_kt * 16;
-      uint16_t* bhi = sB + (r_nt * 16 + 8 + r_g) * kPfLdB + r_kt * 16;
-      reinterpret_cast<u32x4*>(blo)[0] = u32x4{lo[0], lo[1], lo[2], lo[3]};
-      reinterpret_cast<u32x4*>(blo)[1] = u32x4{lo[4], lo[5], lo[6], lo[7]};
-      reinterpret_cast<u32x4*>(bhi)[0] = u32x4{hi[0], hi[1], hi[2], hi[3]};
-      reinterpret_cast<u32x4*>(bhi)[1] = u32x4{hi[4], hi[5], hi[6], hi[7]};
-    }
-    __syncthreads();
-    // ---- MFMA: 2 k-slices of 32 x (2 row tiles x 8 column tiles) ----
-    const int fr = lane & 15, fk = (lane >> 4) * 8;
+    } else {
+      const uint16_t* sb = sB[s & 1];
 #pragma unroll
-    for (int ks = 0; ks < kPfBK; ks += 32) {
-      f16x8 A[2];
+      for (int sl = 0; sl < 2; ++sl) {
+        const int g = 2 * s + sl;
+        if (g + 1 < nslices) load_A(g + 1, Anext);
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
-        A[i] = __builtin_bit_cast(
-            f16x8, *reinterpret_cast<const u32x4*>(sA + (wave * kPfRowsW + i * 16 + fr) * kPfLdA + ks + fk));
+        for (int j = 0; j < 8; ++j) {
+          const f16x8 B = __builtin_bit_cast(
+              f16x8, *reinterpret_cast<const u32x4*>(sb + (j * 16 + c) * kPfLdB + sl * 32 + 8 * q));
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const f16x8 B =
-            __builtin_bit_cast(f16x8, *reinterpret_cast<const u32x4*>(sB + (j * 16 + fr) * kPfLdB + ks + fk));
+          for (int i = 0; i < 4; ++i)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, Acur[i]), B, acc[i][j],
+                                                               0, 0, 0);
+        }
 #pragma unroll
-        for (int i = 0; i < 2; ++i) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[i], B, acc[i][j], 0, 0, 0);
+        for (int i = 0; i < 4; ++i) Acur[i] = Anext[i];
       }
     }
     __syncthreads();
   }
+  if (decoder) return;
 
-  // ---- epilogue: per row, 128-point FWHT over the tile's columns, 1/sqrt(128), svh, bias ----
-  // accumulator layout: lane l holds rows 4*(l/16) + r, column l%16 of each 16 x 16 tile
+  // ---------------- epilogue (MFMA wavefronts) ----------------
+  // acc[i][j][r] = row 16 i + 4 q + r, column 16 j + c of the tile; FWHT over the 128 columns of each row:
+  // column index = 16 j + c, so stages 1..8 pair lanes c ^ h (within the 16-lane group), 16..64 pair j ^ (h/16)
+  const int colbase = nb * 128 + c;
+  float sv[8], bs[8];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int j = 0; j < 8; ++j) {
+    sv[j] = f16_to_f32(svh[colbase + 16 * j]);
+    bs[j] = bias ? load_as_f32<OT>(bias, colbase + 16 * j) : 0.f;
+  }
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
+  for (int i = 0; i < 4; ++i) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) sC[wave][i * 16 + (lane >> 4) * 4 + r][j * 16 + (lane & 15)] = acc[i][j][r];
-  __syncthreads();
-  for (int rr = 0; rr < kPfRowsW; ++rr) {
-    const int gr = row0 + wave * kPfRowsW + rr;
-    float v0 = sC[wave][rr][2 * lane], v1 = sC[wave][rr][2 * lane + 1];
-    {
-      const float s0 = v0 + v1, d0 = v0 - v1;
-      v0 = s0;
-      v1 = d0;
-    }
+    for (int r = 0; r < 4; ++r) {
+      float v[8];
 #pragma unroll
-    for (int h = 1; h < 64; h <<= 1) {
-      const float p0 = __shfl_xor(v0, h), p1 = __shfl_xor(v1, h);
-      if (lane & h) {
-        v0 = p0 - v0;
-        v1 = p1 - v1;
-      } else {
-        v0 = v0 + p0;
-        v1 = v1 + p1;
+      for (int j = 0; j < 8; ++j) v[j] = acc[i][j][r];
+#pragma unroll
+      for (int h = 1; h < 16; h <<= 1) {
+        const bool upper = (c & h) != 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float p = __shfl_xor(v[j], h);
+          v[j] = upper ? p - v[j] : v[j] + p;
+        }
       }
-    }
-    if (gr < rows) {
-      const int col = nb * 128 + 2 * lane;
-      float y0 = round_through<OT>(v0 * kHadScale * f16_to_f32(svh[col]));
-      float y1 = round_through<OT>(v1 * kHadScale * f16_to_f32(svh[col + 1]));
-      if (bias) {
-        y0 = y0 + load_as_f32<OT>(bias, col);
-        y1 = y1 + load_as_f32<OT>(bias, col + 1);
+#pragma unroll
+      for (int hj = 1; hj < 8; hj <<= 1) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          if ((j & hj) == 0) {
+            const float a = v[j], b = v[j + hj];
+            v[j] = a + b;
+            v[j + hj] = a - b;
+          }
+        }
       }
-      store_from_f32<OT>(y, (size_t)gr * n + col, y0);
-      store_from_f32<OT>(y, (size_t)gr * n + col + 1, y1);
+      const int gr = wrow0 + 16 * i + 4 * q + r;
+      if (gr < rows) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          float o = round_through<OT>(v[j] * kHadScale * sv[j]);
+          if (bias) o = o + bs[j];
+          store_from_f32<OT>(y, (size_t)gr * n + colbase + 16 * j, o);
+        }
+      }
     }
   }
 }
@@ -145,9 +211,9 @@ template <int K, int CB>
 static void launch_prefill_ot(int ot, const uint16_t* xh, const uint32_t* tr, int k, int n, int rows,
                               const uint16_t* svh, const void* bias, void* y, hipStream_t st) {
   const dim3 grid((unsigned)(n / 128), (unsigned)((rows + kPfBM - 1) / kPfBM));
-  if (ot == kF16) prefill_kernel<K, CB, kF16><<<grid, 256, 0, st>>>(xh, tr, k, n, rows, svh, bias, y);
-  else if (ot == kBF16) prefill_kernel<K, CB, kBF16><<<grid, 256, 0, st>>>(xh, tr, k, n, rows, svh, bias, y);
-  else prefill_kernel<K, CB, kF32><<<grid, 256, 0, st>>>(xh, tr, k, n, rows, svh, bias, y);
+  if (ot == kF16) prefill_kernel<K, CB, kF16><<<grid, kPfThreads, 0, st>>>(xh, tr, k, n, rows, svh, bias, y);
+  else if (ot == kBF16) prefill_kernel<K, CB, kBF16><<<grid, kPfThreads, 0, st>>>(xh, tr, k, n, rows, svh, bias, y);
+  else prefill_kernel<K, CB, kF32><<<grid, kPfThreads, 0, st>>>(xh, tr, k, n, rows, svh, bias, y);
 }
 
 template <int K>
@@ -175,6 +241,8 @@ extern "C" int exl3_prefill_gemm(const uint16_t* xh, const uint32_t* trellis, in
   EXL3_REQUIRE(aligned(xh, 16) && aligned(trellis, 4), EXL3_ERR_ARG,
                "exl3_prefill_gemm: xh must be 16-byte and trellis 4-byte aligned");
   EXL3_REQUIRE((rows + kPfBM - 1) / kPfBM <= 65535, EXL3_ERR_ARG, "exl3_prefill_gemm: too many rows");
+  EXL3_REQUIRE((uint64_t)rows * (uint64_t)k * 2u < (1ull << 31), EXL3_ERR_ARG,
+               "exl3_prefill_gemm: activations exceed 2 GiB (rows x k)");
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (K) {
     case 1: launch_prefill_cb<1>(cb, out_dtype, xh, trellis, k, n, rows, svh, bias, y, st); break;
