@@ -295,6 +295,8 @@ def main() -> int:
     ap.add_argument("--decoder-layers", type=int, default=64, help="layers of the end-to-end decoder (0 = skip)")
     ap.add_argument("--prompt", type=int, default=512)
     ap.add_argument("--no-configs", action="store_true", help="skip the mixed-K (config 3) and prefill (config 4) lines")
+    ap.add_argument("--only", choices=["prefill", "mixed", "decode"],
+                    help="run one measurement alone and print its JSON (for profiling)")
     ap.add_argument("--gen", type=int, default=256)
     args = ap.parse_args()
 
@@ -324,6 +326,14 @@ def main() -> int:
         return 0
 
     pk = _import_package()
+    if args.only:
+        if args.only == "prefill":
+            print(json.dumps(prefill_benchmark(pk, torch, dev)))
+        elif args.only == "mixed":
+            print(json.dumps(mixed_k_benchmark(pk, torch, dev)))
+        else:
+            print(json.dumps(decode_benchmark(pk, torch, dev, args.decoder_layers, args.prompt, args.gen)))
+        return 0
     K, cb, rows = 6, 0, 1
     fast = args.mode == "fast"
     g = torch.Generator(device=dev).manual_seed(1234)

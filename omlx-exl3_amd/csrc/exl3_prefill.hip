@@ -10,9 +10,9 @@
 //   decode wavefronts (4-7): one trellis run per lane per step (4 k-tiles x 8 n-tiles x 8 runs = 256 runs),
 //     prefetched two steps ahead, decoded into the next step's half of a double-buffered LDS weight tile
 //     (n-major, 16-byte pair groups, the B-operand layout of v_mfma_f32_16x16x32_f16);
-//   MFMA wavefronts (0-3): 64 rows each; activations loaded straight into A-operand registers one 32-k
-//     slice ahead (rows past the batch read zero through the buffer descriptor), 64 MFMAs per step against
-//     the current half of the weight tile.
+//   MFMA wavefronts (0-3): 64 rows each; activations loaded straight into A-operand registers two 32-k
+//     slices ahead (a ring of three; rows past the batch read zero through the buffer descriptor), 64 MFMAs
+//     per step against the current half of the weight tile.
 // One barrier per step hands the tile halves over, so decoding (VALU) overlaps the matrix work (MFMA) on
 // the same SIMDs. Epilogue: the 128-point FWHT of each row runs in registers (stages 1, 2, 4, 8 across the 16
 // lanes of a column group, 16, 32, 64 across the accumulator tiles of a lane), then 1/sqrt(128), svh, bias.
@@ -87,16 +87,16 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const uint16_t* __r
   const __amdgpu_buffer_rsrc_t rs_x = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(xh), (short)0, (int)((uint32_t)rows * (uint32_t)k * 2u), kBufferFlags);
   // A fragments of 32-k slice `g` (= step g / 2, half g % 2) for the 4 row tiles
+  // Rows past the batch and k past the row get an offset past the descriptor, so the load itself returns
+  // zeros (selecting the address, not the loaded value, keeps the load a prefetch: nothing waits for it).
+  const uint32_t oob = (uint32_t)rows * (uint32_t)k * 2u;
   auto load_A = [&](int g, u32x4 (&A)[4]) {
     const int kk = g * 32 + 8 * q;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = wrow0 + 16 * i + c;
-      // rows past the batch lie past the descriptor (zero); k past the row is zeroed explicitly
-      const uint32_t off = (uint32_t)(r < rows ? r : rows) * (uint32_t)k * 2u + (uint32_t)kk * 2u;
-      u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs_x, off, 0u, 0);
-      if (kk >= k) v = u32x4{0u, 0u, 0u, 0u};
-      A[i] = v;
+      const uint32_t off = (r < rows && kk < k) ? (uint32_t)r * (uint32_t)k * 2u + (uint32_t)kk * 2u : oob;
+      A[i] = __builtin_amdgcn_raw_buffer_load_b128(rs_x, off, 0u, 0);
     }
   };
 
@@ -108,7 +108,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const uint16_t* __r
 
   // ---------------- pipeline ----------------
   uint32_t w0[K], w1[K], wp0 = 0, wp1 = 0;   // decode: words of steps s+1 (w0) and s+2 (w1)
-  u32x4 Acur[4], Anext[4];
+  u32x4 Aring[3][4];                          // A fragments of slices g, g+1, g+2
   if (decoder) {
     uint32_t w[K], wp;
     load_run_words(0, w, wp);
@@ -116,13 +116,18 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const uint16_t* __r
     load_run_words(2, w1, wp1);
     store_run(0, 0, w, wp);
   } else {
-    load_A(0, Acur);
+    load_A(0, Aring[0]);
+    load_A(1, Aring[1]);
   }
   __syncthreads();
-  const int nslices = 2 * nsteps;
 
-  for (int s = 0; s < nsteps; ++s) {
-    if (decoder) {
+  // The two roles run separate loops with one barrier per step each (same count), so the compiler's wait
+  // analysis of one role never sees the other role's loads. The step count is padded to a multiple of three
+  // (the MFMA loop's unroll): padded steps decode nothing and contract zero activations (k past the matrix
+  // reads zeros) with the finite weights still in LDS, which adds exactly zero.
+  const int nsteps_pad = (nsteps + 2) / 3 * 3;
+  if (decoder) {
+    for (int s = 0; s < nsteps_pad; ++s) {
       if (s + 1 < nsteps) {
         uint32_t w[K], wp;
 #pragma unroll
@@ -134,28 +139,34 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const uint16_t* __r
         load_run_words(s + 3, w1, wp1);
         store_run((s + 1) & 1, s + 1, w, wp);
       }
-    } else {
+      __syncthreads();
+    }
+    return;
+  }
+  // MFMA role: steps in groups of three so that the six slices of a group use the A ring slots at
+  // compile-time indices (slice g in slot g % 3): no register copies, so no wait on loads still in flight.
+  for (int s0 = 0; s0 < nsteps_pad; s0 += 3) {
+    static_for<0, 3>([&](auto D) {
+      constexpr int d = decltype(D)::value;
+      const int s = s0 + d;
       const uint16_t* sb = sB[s & 1];
-#pragma unroll
-      for (int sl = 0; sl < 2; ++sl) {
-        const int g = 2 * s + sl;
-        if (g + 1 < nslices) load_A(g + 1, Anext);
+      static_for<0, 2>([&](auto SL) {
+        constexpr int sl = decltype(SL)::value;
+        constexpr int slot = (2 * d + sl) % 3, pre = (2 * d + sl + 2) % 3;
+        load_A(2 * s + sl + 2, Aring[pre]);   // past the last slice: zeros, never used
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           const f16x8 B = __builtin_bit_cast(
               f16x8, *reinterpret_cast<const u32x4*>(sb + (j * 16 + c) * kPfLdB + sl * 32 + 8 * q));
 #pragma unroll
           for (int i = 0; i < 4; ++i)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, Acur[i]), B, acc[i][j],
-                                                               0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, Aring[slot][i]), B,
+                                                               acc[i][j], 0, 0, 0);
         }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) Acur[i] = Anext[i];
-      }
-    }
-    __syncthreads();
+      });
+      __syncthreads();
+    });
   }
-  if (decoder) return;
 
   // ---------------- epilogue (MFMA wavefronts) ----------------
   // acc[i][j][r] = row 16 i + 4 q + r, column 16 j + c of the tile; FWHT over the 128 columns of each row:
