@@ -145,24 +145,34 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const uint16_t* __r
   }
   // MFMA role: steps in groups of three so that the six slices of a group use the A ring slots at
   // compile-time indices (slice g in slot g % 3): no register copies, so no wait on loads still in flight.
+  // Within a step, the 16 weight fragments (2 slices x 8 column tiles) are read through a ring of three,
+  // two fragments ahead of the MFMAs that use them; scheduling barriers keep that order, so LDS latency
+  // hides behind matrix work instead of stalling it.
+  const uint16_t* bbase = sB[0] + c * kPfLdB + 8 * q;
+  constexpr int kBufHalves = 128 * kPfLdB;
+  auto read_B = [&](int buf, int f) {
+    return *reinterpret_cast<const u32x4*>(bbase + buf * kBufHalves + ((f & 7) * 16) * kPfLdB + (f >> 3) * 32);
+  };
   for (int s0 = 0; s0 < nsteps_pad; s0 += 3) {
     static_for<0, 3>([&](auto D) {
       constexpr int d = decltype(D)::value;
       const int s = s0 + d;
-      const uint16_t* sb = sB[s & 1];
-      static_for<0, 2>([&](auto SL) {
-        constexpr int sl = decltype(SL)::value;
-        constexpr int slot = (2 * d + sl) % 3, pre = (2 * d + sl + 2) % 3;
-        load_A(2 * s + sl + 2, Aring[pre]);   // past the last slice: zeros, never used
+      const int buf = s & 1;
+      u32x4 Bring[3];
+      Bring[0] = read_B(buf, 0);
+      Bring[1] = read_B(buf, 1);
+      static_for<0, 16>([&](auto F) {
+        constexpr int f = decltype(F)::value;
+        constexpr int sl = f >> 3, j = f & 7;
+        constexpr int slot = (2 * d + sl) % 3;
+        if constexpr (j == 0) load_A(2 * s + sl + 2, Aring[(2 * d + sl + 2) % 3]);   // past the end: zeros
+        if constexpr (f + 2 < 16) Bring[(f + 2) % 3] = read_B(buf, f + 2);
+        const f16x8 B = __builtin_bit_cast(f16x8, Bring[f % 3]);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const f16x8 B = __builtin_bit_cast(
-              f16x8, *reinterpret_cast<const u32x4*>(sb + (j * 16 + c) * kPfLdB + sl * 32 + 8 * q));
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, Aring[slot][i]), B,
-                                                               acc[i][j], 0, 0, 0);
-        }
+        for (int i = 0; i < 4; ++i)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, Aring[slot][i]), B, acc[i][j],
+                                                             0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
       });
       __syncthreads();
     });
