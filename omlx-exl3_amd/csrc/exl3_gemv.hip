@@ -4,9 +4,12 @@
 //
 // Work decomposition
 //   grid (blocks, S): workgroup (blk, s) owns one 128-column output block (8 n-tiles, the Hadamard unit)
-//   and the s-th contiguous k-range of kt_per_split k-tiles. 256 threads = 4 wavefronts; wavefront w owns
-//   n-tiles 2w, 2w+1 of the block. Lane l = 16q + c decodes run g = c%8 of n-tile (2w + c/8) for k-tile
+//   and the s-th contiguous k-range of kt_per_split k-tiles. 256 x WK threads = 4 column groups x WK
+//   k-groups of one wavefront; wavefront (cw, kg) owns n-tiles 2cw, 2cw+1 of the block and the split's
+//   iterations kg, kg + WK, ... Lane l = 16q + c decodes run g = c%8 of n-tile (2cw + c/8) for k-tile
 //   (kt0 + 4i + q) in iteration i: one wavefront iteration streams 8 tiles (4 k-tiles x 2 n-tiles).
+//   WK (1 or 2; the kernel takes any) depends only on the shape: narrow outputs have few workgroups, and
+//   more k-groups give each SIMD more wavefronts to interleave.
 //
 // Contraction on MFMA (v_mfma_f32_16x16x32_f16): the decoded weights of a lane are the B operand as they
 // come out of the decoder (lane l = column c, k-group q), the activations are the A operand (row = batch
@@ -17,7 +20,8 @@
 //   register holds that weight's activation twice, so the sum a + b happens inside the MFMA (unrounded)
 //   and the decoder saves its fp16 add.
 //
-// Reduction: wavefronts hold disjoint columns; across the S workgroups of a block the partial sums go to
+// Reduction: the k-groups of a column group add their sums in LDS in k-group order; column groups hold
+// disjoint columns; across the S workgroups of a block the partial sums go to
 // the workspace and the last workgroup to arrive (device-scope counter) adds them in split order 0..S-1,
 // applies the 128-point Hadamard transform (stages 1, 2, ..., 64), 1/sqrt(128), svh, bias, and writes y.
 // The counter is reset by that workgroup, so it is zero again at rest. Fixed order throughout: bitwise
@@ -29,16 +33,24 @@
 namespace exl3 {
 
 template <int K, int CB, int L, int OT>
-__global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
+__global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
   constexpr bool SPLIT = L == kSplit;
   constexpr int TW = 8 * K;
   constexpr int D = kDepth;
   static_assert(D % 2 == 0, "activation registers alternate by phase parity");
-  extern __shared__ u32x4 xs[];   // split's activations: [(iters+1)*4 k-tiles][rows] records of 32 B + zero record
+  // 16-byte units per activation record: 16 fp16 (kPair), or each fp16 twice (kSplit, the A operands as
+  // the MFMAs take them, so the loop spends no permutes on them)
+  constexpr int RW = SPLIT ? 4 : 2;
+  extern __shared__ u32x4 xs[];   // split's activations: [(iters+WK)*4 k-tiles][rows] records + zero record
   __shared__ float bv[kMaxRows][128];
   __shared__ uint32_t last;
 
+  // 256 x WK threads: wavefront w serves column group cw = w % 4 (two n-tiles) and k-group kg = w / 4, which
+  // takes the split's iterations kg, kg + WK, kg + 2 WK, ...; the k-groups' sums are added in LDS in k-group
+  // order. More k-groups put more wavefronts on each SIMD for narrow outputs without adding split-K traffic.
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int nthr = blockDim.x, WK = nthr >> 8;
+  const int cw = wave & 3, kg = wave >> 2;
   const int blk = blockIdx.x, s = blockIdx.y;
   const int m = (blk >= a.blk_end[0]) + (blk >= a.blk_end[1]);
   const int blk0 = m == 0 ? 0 : a.blk_end[m - 1];
@@ -49,17 +61,19 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   const int kt1 = min(a.KT, kt0 + a.kt_per_split);
   const int nkt = kt1 - kt0;
   const int iters = (nkt + 3) >> 2;
+  const int my_iters = iters > kg ? (iters - kg + WK - 1) / WK : 0;   // this k-group's iterations
 
   const int q = lane >> 4, c = lane & 15, g = c & 7;
-  const int nt_local = (blk - blk0) * 8 + wave * 2 + (c >> 3);
+  const int nt_local = (blk - blk0) * 8 + cw * 2 + (c >> 3);
   const uint32_t kstride = (uint32_t)NT * TW;   // words per k-tile row of the member's trellis
   // trellis of this split: k-tile rows [kt0, kt1); lane q of iteration it reads row kt0 + 4 it + q. The
   // descriptor ends at the split's end: prefetches past it (and k-tiles past it) read zeros, no traffic.
   const __amdgpu_buffer_rsrc_t rs_t = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint32_t*>(tr + (size_t)kt0 * kstride), (short)0, (int)((uint32_t)nkt * kstride * 4u), kBufferFlags);
-  const uint32_t vo_t = ((uint32_t)q * kstride + (uint32_t)nt_local * TW + K * g) * 4u;
-  const uint32_t vo_wp = ((uint32_t)q * kstride + (uint32_t)nt_local * TW + (K * g + TW - 1) % TW) * 4u;
-  const uint32_t step_t = 16u * kstride;          // bytes per iteration (4 k-tile rows)
+  // local iteration j of this k-group is the split's iteration kg + WK j
+  const uint32_t vo_t = ((uint32_t)(q + 4 * kg) * kstride + (uint32_t)nt_local * TW + K * g) * 4u;
+  const uint32_t vo_wp = ((uint32_t)(q + 4 * kg) * kstride + (uint32_t)nt_local * TW + (K * g + TW - 1) % TW) * 4u;
+  const uint32_t step_t = 16u * kstride * (uint32_t)WK;   // bytes per local iteration (4 WK k-tile rows)
 
   auto issue_it = [&](Stage<K>& st, int it) {
     // the advance goes into the per-lane offset, which the descriptor's range check covers
@@ -73,18 +87,26 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     __builtin_amdgcn_sched_barrier(0);
   });
 
-  // ---- stage this split's activations in LDS (natural layout), zero past the split ----
-  // record (kl, r) = the 16 activations of k-tile kt0 + kl for batch row r; one extra iteration of zero
+  // ---- stage this split's activations in LDS, zero past the split ----
+  // record (kl, r) = the 16 activations of k-tile kt0 + kl for batch row r; WK extra iterations of zero
   // records (read by the last phase's look-ahead) and a zero record for absent rows at the end
-  const int nrec = (iters + 1) * 4 * rows;
+  const int nrec = (iters + WK) * 4 * rows;
   {
     const uint16_t* __restrict__ xh = a.xh + (size_t)m * rows * a.k;
-    for (int idx = tid; idx < (nrec + 1) * 2; idx += 256) {
-      const int rec = idx >> 1, h = idx & 1;
+    for (int idx = tid; idx < (nrec + 1) * RW; idx += nthr) {
+      const int rec = idx / RW, h = idx % RW;
       u32x4 v = {0u, 0u, 0u, 0u};
       if (rec < nrec) {
         const int kl = rec / rows, r = rec - kl * rows;
-        if (kl < nkt) v = reinterpret_cast<const u32x4*>(xh + (size_t)r * a.k + (size_t)(kt0 + kl) * 16)[h];
+        if (kl < nkt) {
+          const uint16_t* src = xh + (size_t)r * a.k + (size_t)(kt0 + kl) * 16;
+          if constexpr (SPLIT) {
+            const uint2 p = reinterpret_cast<const uint2*>(src)[h];   // activations 4h .. 4h+3
+            v = dup4(p.x, p.y);
+          } else {
+            v = reinterpret_cast<const u32x4*>(src)[h];
+          }
+        }
       }
       xs[idx] = v;
     }
@@ -93,12 +115,12 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
 
   // A operand of lane (q, c): batch row c of k-tile kt0 + 4 it + q; absent rows read the zero record
   const bool active = c < rows;
-  const u32x4* xa = xs + (active ? (size_t)(q * rows + c) * 2 : (size_t)nrec * 2);
-  const int xa_step = active ? 4 * rows * 2 : 0;
-  auto read_A = [&](int it, u32x4 (&A)[2]) {
+  const u32x4* xa = xs + (active ? (size_t)((q + 4 * kg) * rows + c) * RW : (size_t)nrec * RW);
+  const int xa_step = active ? 4 * rows * RW * WK : 0;
+  auto read_A = [&](int it, u32x4 (&A)[RW]) {
     const u32x4* p = xa + (size_t)it * xa_step;
-    A[0] = p[0];
-    A[1] = p[1];
+#pragma unroll
+    for (int i = 0; i < RW; ++i) A[i] = p[i];
   };
 
   const uint32_t xor_v = kXor3;
@@ -108,18 +130,17 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_f16x8(A), as_f16x8(B), acc, 0, 0, 0);
   };
 
-  auto process = [&](const Stage<K>& st, const u32x4 (&X)[2]) {
+  auto process = [&](const Stage<K>& st, const u32x4 (&X)[RW]) {
     if constexpr (SPLIT) {
       uint32_t b[32];
       decode_run<K, CB, true>(st.w, st.wp, b, xor_v);
-      // A_j = activations k = 4j..4j+3, each twice; B = the summand registers of those k:
+      // X[j] = activations k = 4j..4j+3, each twice; B = the summand registers of those k:
       // k 4j, 4j+1 are positions 16(j%2) + 2(j/2) + {0, 1}, k 4j+2, 4j+3 positions 16(j%2) + 8 + 2(j/2) + {0, 1}
-      const u32x4 A[4] = {dup4(X[0].x, X[0].y), dup4(X[0].z, X[0].w), dup4(X[1].x, X[1].y), dup4(X[1].z, X[1].w)};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int p0 = 16 * (j & 1) + 2 * (j >> 1);
-        mfma(acc_lo, A[j], mfma_src(b[p0], b[p0 + 1], b[p0 + 8], b[p0 + 9]));
-        mfma(acc_hi, A[j], mfma_src(b[p0 + 4], b[p0 + 5], b[p0 + 12], b[p0 + 13]));
+        mfma(acc_lo, X[j], mfma_src(b[p0], b[p0 + 1], b[p0 + 8], b[p0 + 9]));
+        mfma(acc_hi, X[j], mfma_src(b[p0 + 4], b[p0 + 5], b[p0 + 12], b[p0 + 13]));
       }
     } else {
       uint32_t b[16];
@@ -137,9 +158,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   // younger sets stay in flight), the remaining < D iterations peeled after it. Each phase reads the next
   // phase's activations from LDS first. Scheduling barriers keep one phase's decode from being hoisted into
   // the previous one, which would make it wait for a set that is still in flight.
-  u32x4 X[2][2];
+  u32x4 X[2][RW];
   read_A(0, X[0]);
-  const int full = iters / D * D;
+  const int full = my_iters / D * D;
   int it = 0;
   for (; it < full; it += D) {
     static_for<0, D>([&](auto P) {
@@ -152,23 +173,27 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   }
   static_for<0, D - 1>([&](auto P) {
     constexpr int d = decltype(P)::value;
-    if (it + d < iters) {
+    if (it + d < my_iters) {
       read_A(it + d + 1, X[(d + 1) & 1]);
       process(st[d], X[d & 1]);
     }
   });
 
-  // ---- columns of this wavefront -> block partial (LDS) ----
-  const int col_lo = (wave * 2 + (c >> 3)) * 16 + g, col_hi = col_lo + 8;
+  // ---- columns of this wavefront -> block partial (LDS), k-groups added in order 0, 1, .., WK-1 ----
+  const int col_lo = (cw * 2 + (c >> 3)) * 16 + g, col_hi = col_lo + 8;
+  for (int t = 0; t < WK; ++t) {
+    if (kg == t) {
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int ro = 4 * q + r;
-    if (ro < rows) {
-      bv[ro][col_lo] = acc_lo[r];
-      bv[ro][col_hi] = acc_hi[r];
+      for (int r = 0; r < 4; ++r) {
+        const int ro = 4 * q + r;
+        if (ro < rows) {
+          bv[ro][col_lo] = t == 0 ? acc_lo[r] : bv[ro][col_lo] + acc_lo[r];
+          bv[ro][col_hi] = t == 0 ? acc_hi[r] : bv[ro][col_hi] + acc_hi[r];
+        }
+      }
     }
+    __syncthreads();
   }
-  __syncthreads();
 
   // ---- k-splits across workgroups: the last arriver sums the partials in split order ----
   // Cross-workgroup traffic uses device-scope relaxed atomic stores and loads, which the hardware performs at
@@ -178,7 +203,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   if (a.S > 1) {
     float* part = a.partials;
     const size_t pstride = (size_t)rows * a.n_total;
-    for (int idx = tid; idx < rows * 128; idx += 256) {
+    for (int idx = tid; idx < rows * 128; idx += nthr) {
       const int r = idx >> 7, cc = idx & 127;
       __hip_atomic_store(part + (size_t)s * pstride + (size_t)r * a.n_total + blk * 128 + cc, bv[r][cc],
                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -192,7 +217,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     }
     __syncthreads();
     if (last == 0) return;
-    for (int idx = tid; idx < rows * 128; idx += 256) {
+    for (int idx = tid; idx < rows * 128; idx += nthr) {
       const int r = idx >> 7, cc = idx & 127;
       bv[r][cc] = sum_splits(part + (size_t)r * a.n_total + blk * 128 + cc, pstride, a.S);
     }
@@ -201,7 +226,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   }
 
   // ---- 128-point FWHT per row (stages 1, 2, ..., 64), 1/sqrt(128), svh, bias ----
-  for (int r = wave; r < rows; r += 4) {
+  for (int r = wave; r < rows; r += nthr >> 6) {
     float v0 = bv[r][2 * lane], v1 = bv[r][2 * lane + 1];
     {
       const float s0 = v0 + v1, d0 = v0 - v1;
@@ -240,7 +265,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
 // A-operand layout for a codebook and flags: MUL1 always contracts fp16-rounded values (pair layout)
 static int layout_for(int cb, unsigned flags) { return (cb == 2 || !(flags & EXL3_GEMV_FAST)) ? kPair : kSplit; }
 
-constexpr int kMaxKtPerSplit = 96;           // staged activations of a split stay within 64 KiB at 16 rows
+constexpr int kMaxKtPerSplit = 96;
+// staged activations: at most 26 iterations x 4 k-tiles x 16 rows x 64 B (+ zero record) = 104 KiB + 64 B
+constexpr size_t kMaxGemvSmem = 112 * 1024;
 
 // k-tiles per split. Measured on MI355X at K = 6 (27B shapes), the GEMV's time is flat within a few percent
 // for splits of 40-96 k-tiles and grows outside that range: shorter splits add partial sums and pipeline
@@ -253,6 +280,12 @@ static int auto_kt_per_split(int KT, int blocks) {
   return kps > ktr ? ktr : kps;
 }
 
+// k-groups per workgroup, from the shape alone (never from the row count). Measured on MI355X at K = 6
+// (27B shapes): two k-groups take 3-12% off the launches of up to 512 workgroups at rows 1 and 10-20% at
+// rows 8; four were slower than two on every shape, and wide launches (1,904 workgroups) are fastest
+// with one.
+static int auto_k_groups(int blocks, int S) { return (long)blocks * S <= 512 ? 2 : 1; }
+
 // workspace: [per-block counters, padded to 256 B][S x rows x n_total fp32 partials]
 static size_t counters_bytes(int blocks) { return ((size_t)blocks * sizeof(uint32_t) + 255) / 256 * 256; }
 
@@ -263,34 +296,46 @@ static size_t workspace_for(int KT, int blocks, int rows, int n_total, int kps) 
   return bytes;
 }
 
+struct GemvLaunch {
+  int blocks, threads;
+  size_t smem;
+  hipStream_t st;
+};
+
 template <int K, int CB, int L, int OT>
-static void launch_gemv(const GemvArgs& a, int blocks, size_t smem, hipStream_t st) {
-  gemv_kernel<K, CB, L, OT><<<dim3(blocks, a.S), 256, smem, st>>>(a);
+static void launch_gemv(const GemvArgs& a, const GemvLaunch& g) {
+  if (g.smem > 64 * 1024) {   // per instantiation; the attribute is a property of the kernel function
+    static const bool attr_ok =
+        hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_kernel<K, CB, L, OT>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxGemvSmem) == hipSuccess;
+    (void)attr_ok;   // a failure surfaces as a launch error
+  }
+  gemv_kernel<K, CB, L, OT><<<dim3(g.blocks, a.S), g.threads, g.smem, g.st>>>(a);
 }
 
 template <int K, int CB, int L>
-static void dispatch_ot(int ot, const GemvArgs& a, int blocks, size_t smem, hipStream_t st) {
-  if (ot == kF16) launch_gemv<K, CB, L, kF16>(a, blocks, smem, st);
-  else if (ot == kBF16) launch_gemv<K, CB, L, kBF16>(a, blocks, smem, st);
-  else launch_gemv<K, CB, L, kF32>(a, blocks, smem, st);
+static void dispatch_ot(int ot, const GemvArgs& a, const GemvLaunch& g) {
+  if (ot == kF16) launch_gemv<K, CB, L, kF16>(a, g);
+  else if (ot == kBF16) launch_gemv<K, CB, L, kBF16>(a, g);
+  else launch_gemv<K, CB, L, kF32>(a, g);
 }
 
 template <int K, int CB>
-static void dispatch_layout(int layout, int ot, const GemvArgs& a, int blocks, size_t smem, hipStream_t st) {
+static void dispatch_layout(int layout, int ot, const GemvArgs& a, const GemvLaunch& g) {
   if constexpr (CB < 2) {
     if (layout == kSplit) {
-      dispatch_ot<K, CB, kSplit>(ot, a, blocks, smem, st);
+      dispatch_ot<K, CB, kSplit>(ot, a, g);
       return;
     }
   }
-  dispatch_ot<K, CB, kPair>(ot, a, blocks, smem, st);
+  dispatch_ot<K, CB, kPair>(ot, a, g);
 }
 
 template <int K>
-static void dispatch_cb(int cb, int layout, int ot, const GemvArgs& a, int blocks, size_t smem, hipStream_t st) {
-  if (cb == 0) dispatch_layout<K, 0>(layout, ot, a, blocks, smem, st);
-  else if (cb == 1) dispatch_layout<K, 1>(layout, ot, a, blocks, smem, st);
-  else dispatch_layout<K, 2>(layout, ot, a, blocks, smem, st);
+static void dispatch_cb(int cb, int layout, int ot, const GemvArgs& a, const GemvLaunch& g) {
+  if (cb == 0) dispatch_layout<K, 0>(layout, ot, a, g);
+  else if (cb == 1) dispatch_layout<K, 1>(layout, ot, a, g);
+  else dispatch_layout<K, 2>(layout, ot, a, g);
 }
 
 }  // namespace exl3
@@ -378,10 +423,17 @@ extern "C" int exl3_gemv_ex(const uint16_t* xh, const uint32_t* const* trellis, 
   }
   const int layout = layout_for(cb, flags);
   const int kps = kt_per_split > 0 ? ((kt_per_split + 3) / 4) * 4 : auto_kt_per_split(KT, blocks);
-  // staged activations: ((iters + 1) * 4 * rows + 1) records of 32 bytes
-  const size_t smem = ((size_t)(kps / 4 + 1) * 4 * rows + 1) * 32;
-  EXL3_REQUIRE(smem <= 64 * 1024, EXL3_ERR_ARG, "exl3_gemv: kt_per_split %d too large for %d rows", kps, rows);
   const int S = (KT + kps - 1) / kps;
+  const int WK = auto_k_groups(blocks, S);
+  // staged activations: ((iters + WK) * 4 * rows + 1) records of 32 bytes (64 in the split layout)
+  const size_t smem = ((size_t)(kps / 4 + WK) * 4 * rows + 1) * (layout == kSplit ? 64 : 32);
+  EXL3_REQUIRE(smem <= kMaxGemvSmem, EXL3_ERR_ARG, "exl3_gemv: kt_per_split %d too large for %d rows", kps, rows);
+  // byte offsets into a split's trellis, look-ahead loads included, stay below 2^32
+  for (int i = 0; i < n_members; ++i) {
+    const uint64_t kstride_bytes = (uint64_t)(member_n[i] / 16) * 8 * K * 4;
+    EXL3_REQUIRE((uint64_t)(kps + 4 * WK * (kDepth + 1)) * kstride_bytes < (1ull << 32), EXL3_ERR_ARG,
+                 "exl3_gemv: member %d (%d x %d) too large for 32-bit trellis offsets", i, k, member_n[i]);
+  }
   const size_t need = workspace_for(KT, blocks, rows, n_total, kps);
   EXL3_REQUIRE(workspace && workspace_bytes >= need && aligned(workspace, 256), EXL3_ERR_WORKSPACE,
                "exl3_gemv: a zero-initialised, 256-byte aligned workspace of %zu bytes is needed (got %zu)", need,
@@ -398,15 +450,16 @@ extern "C" int exl3_gemv_ex(const uint16_t* xh, const uint32_t* const* trellis, 
   a.n_total = n_total;
   a.S = S;
   a.kt_per_split = kps;
+  const GemvLaunch g{blocks, 256 * WK, smem, st};
   switch (K) {
-    case 1: dispatch_cb<1>(cb, layout, out_dtype, a, blocks, smem, st); break;
-    case 2: dispatch_cb<2>(cb, layout, out_dtype, a, blocks, smem, st); break;
-    case 3: dispatch_cb<3>(cb, layout, out_dtype, a, blocks, smem, st); break;
-    case 4: dispatch_cb<4>(cb, layout, out_dtype, a, blocks, smem, st); break;
-    case 5: dispatch_cb<5>(cb, layout, out_dtype, a, blocks, smem, st); break;
-    case 6: dispatch_cb<6>(cb, layout, out_dtype, a, blocks, smem, st); break;
-    case 7: dispatch_cb<7>(cb, layout, out_dtype, a, blocks, smem, st); break;
-    default: dispatch_cb<8>(cb, layout, out_dtype, a, blocks, smem, st); break;
+    case 1: dispatch_cb<1>(cb, layout, out_dtype, a, g); break;
+    case 2: dispatch_cb<2>(cb, layout, out_dtype, a, g); break;
+    case 3: dispatch_cb<3>(cb, layout, out_dtype, a, g); break;
+    case 4: dispatch_cb<4>(cb, layout, out_dtype, a, g); break;
+    case 5: dispatch_cb<5>(cb, layout, out_dtype, a, g); break;
+    case 6: dispatch_cb<6>(cb, layout, out_dtype, a, g); break;
+    case 7: dispatch_cb<7>(cb, layout, out_dtype, a, g); break;
+    default: dispatch_cb<8>(cb, layout, out_dtype, a, g); break;
   }
   EXL3_LAUNCH_CHECK("exl3_gemv");
   return EXL3_OK;
