@@ -102,6 +102,36 @@ int exl3_gemv_ex(const uint16_t* xh, const uint32_t* const* trellis, int n_membe
                  int k, int K, int cb, const uint16_t* svh, const void* bias, void* y, int out_dtype, int rows,
                  unsigned flags, void* workspace, size_t workspace_bytes, int kt_per_split, void* stream);
 
+/* exl3_gemv with the decoder's neighbouring element-wise steps inside the same launch, so the norm,
+ * SwiGLU and residual-add launches around the GEMVs of a decode step disappear. No counterpart in the
+ * reference, which runs norm_rot / swiglu_rot (kernels.py:408-433), the GEMV, and leaves the residual add to
+ * the model graph as separate launches; the values are those of exl3_rmsnorm_rotate / exl3_swiglu_rotate
+ * (fp16) and exl3_gemv, bit for bit. Always the hashing kernel.
+ * Prologue (how the rotated input is formed):
+ *   EXL3_PROLOGUE_NONE     x is the rotated input xh (n_members, rows, k), as exl3_gemv's; residual,
+ *                          residual_out, w, x_sumsq and suh NULL
+ *   EXL3_PROLOGUE_RMSNORM  x fp16 (rows, k); residual NULL or fp16 (rows, k); h = fp16(x + residual) is
+ *                          written to residual_out (NULL: not written; must not overlap x or residual);
+ *                          w fp16 (k), eps: xh_m = rot(fp16(w * fp16(h * rsqrt(mean(h^2) + eps))), suh_m).
+ *                          x_sumsq: NULL, or with no residual the sums of squares of x's 128-blocks
+ *                          (rows, k/128) fp64 as a previous call's y_sumsq wrote them, so the launch reads
+ *                          only its own part of x
+ *   EXL3_PROLOGUE_SWIGLU   x = gu fp16 (rows, 2k) = [gate | up], one member: xh = rot(silu(gate) * up, suh);
+ *                          residual, residual_out, w and x_sumsq NULL
+ *   suh fp16 (n_members, k); k % 128 == 0 with a prologue.
+ * Epilogue (fp16 output only): y = fp16(y + y_residual) when y_residual (rows, n_total) is given (the next
+ * norm's residual add; y_residual may be y's own buffer), and y_sumsq (rows, n_total/128) fp64 receives each
+ * 128-column block's sum of squares of y when given. The other arguments as exl3_gemv. */
+#define EXL3_PROLOGUE_NONE 0
+#define EXL3_PROLOGUE_RMSNORM 1
+#define EXL3_PROLOGUE_SWIGLU 2
+int exl3_gemv_fused(int prologue, const uint16_t* x, const uint16_t* residual, uint16_t* residual_out,
+                    const uint16_t* w, float eps, const double* x_sumsq, const uint16_t* suh,
+                    const uint32_t* const* trellis, int n_members, const int* member_n, int k, int K, int cb,
+                    const uint16_t* svh, const void* bias, void* y, int out_dtype, int rows, unsigned flags,
+                    const uint16_t* y_residual, double* y_sumsq, void* workspace, size_t workspace_bytes,
+                    void* stream);
+
 /* Input rotation: xh[m, r, :] = fp16(H128(x[r, :] * suh[m, :]) / sqrt(128)) per 128-block, fp32 inside.
  * Replaces rot (kernels.py:388-406, 451-458). x (rows, k) in x_dtype; suh fp16 (n_members, k);
  * xh fp16 (n_members, rows, k). k % 128 == 0. */

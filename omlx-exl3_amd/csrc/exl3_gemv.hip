@@ -32,6 +32,117 @@
 
 namespace exl3 {
 
+// Prologue staging: the split's activations computed in the workgroup from the layer's un-rotated input
+// instead of read from xh. kProNorm: h = fp16(x + residual) and xn = fp16(w * fp16(h * inv_rms)) with the row's
+// sum of squares in fp64 (exact, so independent of the reduction order), as exl3_rmsnorm_rotate computes them;
+// kProSwiglu: silu(gate) * up as exl3_swiglu_rotate computes it. Then e = v * suh_m, the 128-point FWHT of
+// each block, * 1/sqrt(128), fp16: the values those kernels write to xh, so the GEMV's result is bit-identical
+// to rotating first. The workgroup of member 0's first block in each split also writes h for the split's
+// k-range. k is a multiple of 128 (checked on the host).
+template <bool SPLIT>
+__device__ void stage_prologue(const GemvArgs& a, int m, int blk_in_member, int kt0, int kt1, int nrec, u32x4* xs,
+                               double (*ss_part)[16], float* inv_rms) {
+  constexpr int RW = SPLIT ? 4 : 2;
+  const int tid = threadIdx.x, nthr = blockDim.x, lane = tid & 63, wave = tid >> 6, nw = nthr >> 6;
+  const int rows = a.rows, k = a.k, nkt = kt1 - kt0;
+  // zero records: k-tiles past the split (read by the look-ahead) and the absent-row record
+  for (int idx = nkt * rows * RW + tid; idx < (nrec + 1) * RW; idx += nthr) xs[idx] = u32x4{0u, 0u, 0u, 0u};
+  if (a.pro == kProNorm && a.pss) {
+    // the producer's per-block sums of squares, added in block order (exact in fp64, like the row sum)
+    if (tid < rows) {
+      double tot = 0.0;
+      for (int b = 0; b < k / 128; ++b) tot += a.pss[(size_t)tid * (k / 128) + b];
+      const float mean = (float)tot / (float)k;
+      const float v = mean + a.eps;
+      inv_rms[tid] = (float)(1.0 / sqrt((double)v));
+    }
+    __syncthreads();
+  } else if (a.pro == kProNorm) {
+    for (int r = 0; r < rows; ++r) {
+      double ss = 0.0;
+      for (int ch = tid; ch < k / 8; ch += nthr) {
+        float hv[8];
+        load8<kF16>(a.px, (size_t)r * k + (size_t)ch * 8, hv);
+        if (a.pres) {
+          float rv[8];
+          load8<kF16>(a.pres, (size_t)r * k + (size_t)ch * 8, rv);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) hv[i] = round_through<kF16>(hv[i] + rv[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ss += (double)hv[i] * (double)hv[i];
+      }
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+      if (lane == 0) ss_part[r][wave] = ss;
+    }
+    __syncthreads();
+    if (tid < rows) {
+      double tot = 0.0;
+      for (int w = 0; w < nw; ++w) tot += ss_part[tid][w];
+      const float mean = (float)tot / (float)k;
+      const float v = mean + a.eps;
+      inv_rms[tid] = (float)(1.0 / sqrt((double)v));
+    }
+    __syncthreads();
+  }
+  const int b0 = kt0 >> 3, b1 = (kt1 + 7) >> 3;   // 128-element blocks overlapping the split
+  const int nb = (b1 - b0) * rows;
+  const bool write_h = a.pro == kProNorm && a.pres_out != nullptr && m == 0 && blk_in_member == 0;
+  const uint16_t* __restrict__ suh = a.psuh + (size_t)m * k;
+  // one 128-block of one row per 16-lane group (8 consecutive elements per lane); a group is active or idle
+  // as a whole, and its FWHT exchanges stay inside the group
+  for (int t = tid >> 4; t < nb; t += nthr >> 4) {
+    const int r = t % rows, b = b0 + t / rows;
+    const int c0 = b * 128 + (lane & 15) * 8;
+    const int kt = c0 >> 4;
+    const bool in_split = kt >= kt0 && kt < kt1;
+    float v[8];
+    if (a.pro == kProNorm) {
+      float wv[8];
+      load8<kF16>(a.px, (size_t)r * k + c0, v);
+      if (a.pres) {
+        float rv[8];
+        load8<kF16>(a.pres, (size_t)r * k + c0, rv);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = round_through<kF16>(v[i] + rv[i]);
+      }
+      if (write_h && in_split) store8<kF16>(a.pres_out, (size_t)r * k + c0, v);
+      load8<kF16>(a.pw, c0, wv);
+      const float inv = inv_rms[r];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = round_through<kF16>(wv[i] * round_through<kF16>(v[i] * inv));
+    } else {
+      float uv[8];
+      load8<kF16>(a.px, (size_t)r * 2 * k + c0, v);
+      load8<kF16>(a.px, (size_t)r * 2 * k + k + c0, uv);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float ex = (float)exp(-(double)v[i]);   // exp(-g) rounded once to fp32
+        v[i] = (v[i] / (1.0f + ex)) * uv[i];
+      }
+    }
+    float sv[8];
+    load8<kF16>(suh, c0, sv);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = v[i] * sv[i];
+    fwht128_lane8(v, lane);
+    if (in_split) {
+      uint32_t d[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        d[j] = (uint32_t)f32_to_f16(v[2 * j] * kHadScale) | ((uint32_t)f32_to_f16(v[2 * j + 1] * kHadScale) << 16);
+      const int rec = (kt - kt0) * rows + r, half = (c0 >> 3) & 1;
+      if constexpr (SPLIT) {
+        xs[rec * 4 + 2 * half] = dup4(d[0], d[1]);
+        xs[rec * 4 + 2 * half + 1] = dup4(d[2], d[3]);
+      } else {
+        xs[rec * 2 + half] = u32x4{d[0], d[1], d[2], d[3]};
+      }
+    }
+  }
+}
+
 template <int K, int CB, int L, int OT>
 __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
   constexpr bool SPLIT = L == kSplit;
@@ -44,6 +155,8 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
   extern __shared__ u32x4 xs[];   // split's activations: [(iters+WK)*4 k-tiles][rows] records + zero record
   __shared__ float bv[kMaxRows][128];
   __shared__ uint32_t last;
+  __shared__ double ss_part[kMaxRows][16];   // prologue: per-wavefront partial sums of squares
+  __shared__ float inv_rms[kMaxRows];
 
   // 256 x WK threads: wavefront w serves column group cw = w % 4 (two n-tiles) and k-group kg = w / 4, which
   // takes the split's iterations kg, kg + WK, kg + 2 WK, ...; the k-groups' sums are added in LDS in k-group
@@ -91,7 +204,9 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
   // record (kl, r) = the 16 activations of k-tile kt0 + kl for batch row r; WK extra iterations of zero
   // records (read by the last phase's look-ahead) and a zero record for absent rows at the end
   const int nrec = (iters + WK) * 4 * rows;
-  {
+  if (a.pro != kProNone) {
+    stage_prologue<SPLIT>(a, m, blk - blk0, kt0, kt1, nrec, xs, ss_part, inv_rms);
+  } else {
     const uint16_t* __restrict__ xh = a.xh + (size_t)m * rows * a.k;
     for (int idx = tid; idx < (nrec + 1) * RW; idx += nthr) {
       const int rec = idx / RW, h = idx % RW;
@@ -250,12 +365,22 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
     y0 = round_through<OT>(y0);
     y1 = round_through<OT>(y1);
     if (a.bias) {
-      y0 = y0 + load_as_f32<OT>(a.bias, col);
-      y1 = y1 + load_as_f32<OT>(a.bias, col + 1);
+      y0 = round_through<OT>(y0 + load_as_f32<OT>(a.bias, col));
+      y1 = round_through<OT>(y1 + load_as_f32<OT>(a.bias, col + 1));
     }
     const size_t o = (size_t)r * a.n_total + col;
+    if (a.eres) {   // residual add of the next RMSNorm (fp16 output)
+      y0 = round_through<OT>(y0 + f16_to_f32(a.eres[o]));
+      y1 = round_through<OT>(y1 + f16_to_f32(a.eres[o + 1]));
+    }
     store_from_f32<OT>(a.y, o, y0);
     store_from_f32<OT>(a.y, o + 1, y1);
+    if (a.ess) {    // this block's sum of squares for the next RMSNorm
+      double ss = (double)y0 * (double)y0 + (double)y1 * (double)y1;
+#pragma unroll
+      for (int h = 32; h >= 1; h >>= 1) ss += __shfl_xor(ss, h);
+      if (lane == 0) a.ess[(size_t)r * (a.n_total / 128) + blk] = ss;
+    }
   }
 }
 
@@ -353,11 +478,25 @@ extern "C" size_t exl3_gemv_workspace_bytes(int k, int n_total, int rows, int K)
   return bytes;
 }
 
-extern "C" int exl3_gemv_ex(const uint16_t* xh, const uint32_t* const* trellis, int n_members, const int* member_n,
-                            int k, int K, int cb, const uint16_t* svh, const void* bias, void* y, int out_dtype,
-                            int rows, unsigned flags, void* workspace, size_t workspace_bytes, int kt_per_split,
-                            void* stream) {
-  EXL3_REQUIRE(xh && trellis && member_n && svh && y, EXL3_ERR_ARG, "exl3_gemv: NULL pointer argument");
+namespace exl3 {
+struct GemvPrologueArgs {
+  int mode;
+  const uint16_t *x, *residual;
+  uint16_t* residual_out;
+  const uint16_t *w, *suh;
+  float eps;
+  const double* x_sumsq;
+  const uint16_t* y_residual;
+  double* y_sumsq;
+};
+}  // namespace exl3
+
+static int gemv_run(const uint16_t* xh, const GemvPrologueArgs& pro, const uint32_t* const* trellis, int n_members,
+                    const int* member_n, int k, int K, int cb, const uint16_t* svh, const void* bias, void* y,
+                    int out_dtype, int rows, unsigned flags, void* workspace, size_t workspace_bytes, int kt_per_split,
+                    void* stream) {
+  EXL3_REQUIRE((xh || pro.mode != kProNone) && trellis && member_n && svh && y, EXL3_ERR_ARG,
+               "exl3_gemv: NULL pointer argument");
   EXL3_REQUIRE(n_members >= 1 && n_members <= 3, EXL3_ERR_ARG, "exl3_gemv: 1..3 members (got %d)", n_members);
   EXL3_REQUIRE(k > 0 && k % 16 == 0, EXL3_ERR_ARG, "exl3_gemv: k must be a positive multiple of 16 (got %d)", k);
   EXL3_REQUIRE(K >= 1 && K <= 8, EXL3_ERR_ARG, "exl3_gemv: K must be 1..8 (got %d)", K);
@@ -387,7 +526,8 @@ extern "C" int exl3_gemv_ex(const uint16_t* xh, const uint32_t* const* trellis, 
   }
   const int KT = k / 16, blocks = n_total / 128;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  bool table_ok = kt_per_split <= 0 && (flags & EXL3_GEMV_TABLE) && gemv_lut_eligible(k, K, cb, flags);
+  bool table_ok = pro.mode == kProNone && kt_per_split <= 0 && (flags & EXL3_GEMV_TABLE) &&
+                  gemv_lut_eligible(k, K, cb, flags);
   for (int i = 0; i < n_members && table_ok; ++i) table_ok = gemv_lut_offsets_fit(k, member_n[i], K);
   if (table_ok) {
     GemvLutArgs b{};
@@ -450,6 +590,16 @@ extern "C" int exl3_gemv_ex(const uint16_t* xh, const uint32_t* const* trellis, 
   a.n_total = n_total;
   a.S = S;
   a.kt_per_split = kps;
+  a.pro = pro.mode;
+  a.px = pro.x;
+  a.pres = pro.residual;
+  a.pres_out = pro.residual_out;
+  a.pw = pro.w;
+  a.eps = pro.eps;
+  a.psuh = pro.suh;
+  a.pss = pro.x_sumsq;
+  a.eres = pro.y_residual;
+  a.ess = pro.y_sumsq;
   const GemvLaunch g{blocks, 256 * WK, smem, st};
   switch (K) {
     case 1: dispatch_cb<1>(cb, layout, out_dtype, a, g); break;
@@ -463,6 +613,65 @@ extern "C" int exl3_gemv_ex(const uint16_t* xh, const uint32_t* const* trellis, 
   }
   EXL3_LAUNCH_CHECK("exl3_gemv");
   return EXL3_OK;
+}
+
+extern "C" int exl3_gemv_ex(const uint16_t* xh, const uint32_t* const* trellis, int n_members, const int* member_n,
+                            int k, int K, int cb, const uint16_t* svh, const void* bias, void* y, int out_dtype,
+                            int rows, unsigned flags, void* workspace, size_t workspace_bytes, int kt_per_split,
+                            void* stream) {
+  const GemvPrologueArgs none{kProNone, nullptr, nullptr, nullptr, nullptr, nullptr, 0.f, nullptr, nullptr, nullptr};
+  return gemv_run(xh, none, trellis, n_members, member_n, k, K, cb, svh, bias, y, out_dtype, rows, flags, workspace,
+                  workspace_bytes, kt_per_split, stream);
+}
+
+extern "C" int exl3_gemv_fused(int prologue, const uint16_t* x, const uint16_t* residual, uint16_t* residual_out,
+                               const uint16_t* w, float eps, const double* x_sumsq, const uint16_t* suh,
+                               const uint32_t* const* trellis, int n_members, const int* member_n, int k, int K,
+                               int cb, const uint16_t* svh, const void* bias, void* y, int out_dtype, int rows,
+                               unsigned flags, const uint16_t* y_residual, double* y_sumsq, void* workspace,
+                               size_t workspace_bytes, void* stream) {
+  EXL3_REQUIRE(prologue == EXL3_PROLOGUE_NONE || prologue == EXL3_PROLOGUE_RMSNORM || prologue == EXL3_PROLOGUE_SWIGLU,
+               EXL3_ERR_ARG, "exl3_gemv_fused: unknown prologue %d", prologue);
+  EXL3_REQUIRE((y_residual == nullptr && y_sumsq == nullptr) || out_dtype == kF16, EXL3_ERR_ARG,
+               "exl3_gemv_fused: y_residual and y_sumsq need an fp16 output");
+  EXL3_REQUIRE(!y_sumsq || aligned(y_sumsq, 8), EXL3_ERR_ARG, "exl3_gemv_fused: y_sumsq must be 8-byte aligned");
+  if (prologue == EXL3_PROLOGUE_NONE) {
+    EXL3_REQUIRE(!residual && !residual_out && !w && !x_sumsq && !suh, EXL3_ERR_ARG,
+                 "exl3_gemv_fused: without a prologue x is the rotated input and the prologue arguments are NULL");
+    const GemvPrologueArgs pro{kProNone, nullptr, nullptr, nullptr, nullptr, nullptr, 0.f, nullptr, y_residual,
+                               y_sumsq};
+    return gemv_run(x, pro, trellis, n_members, member_n, k, K, cb, svh, bias, y, out_dtype, rows, flags, workspace,
+                    workspace_bytes, 0, stream);
+  }
+  EXL3_REQUIRE(x && suh, EXL3_ERR_ARG, "exl3_gemv_fused: NULL x or suh");
+  EXL3_REQUIRE(k > 0 && k % 128 == 0, EXL3_ERR_ARG, "exl3_gemv_fused: k must be a positive multiple of 128 (got %d)",
+               k);
+  EXL3_REQUIRE(aligned(x, 16) && aligned(suh, 16) && (!residual || aligned(residual, 16)) &&
+                   (!residual_out || aligned(residual_out, 16)) && (!w || aligned(w, 16)),
+               EXL3_ERR_ARG, "exl3_gemv_fused: x, residual, residual_out, w and suh must be 16-byte aligned");
+  if (prologue == EXL3_PROLOGUE_RMSNORM) {
+    EXL3_REQUIRE(w != nullptr, EXL3_ERR_ARG, "exl3_gemv_fused: RMSNORM needs the norm weight");
+    EXL3_REQUIRE(residual_out == nullptr || residual != nullptr, EXL3_ERR_ARG,
+                 "exl3_gemv_fused: residual_out needs a residual");
+    EXL3_REQUIRE(x_sumsq == nullptr || (residual == nullptr && aligned(x_sumsq, 8)), EXL3_ERR_ARG,
+                 "exl3_gemv_fused: x_sumsq (8-byte aligned) describes x alone, so it takes no residual");
+    if (residual_out) {   // other workgroups read x and residual while h is written
+      const size_t bytes = (size_t)rows * k * 2;
+      auto overlaps = [&](const void* p) {
+        const char *a0 = static_cast<const char*>(p), *b0 = reinterpret_cast<const char*>(residual_out);
+        return a0 < b0 + bytes && b0 < a0 + bytes;
+      };
+      EXL3_REQUIRE(!overlaps(x) && !overlaps(residual), EXL3_ERR_ARG,
+                   "exl3_gemv_fused: residual_out must not overlap x or residual");
+    }
+  } else {
+    EXL3_REQUIRE(n_members == 1 && residual == nullptr && residual_out == nullptr && x_sumsq == nullptr, EXL3_ERR_ARG,
+                 "exl3_gemv_fused: SWIGLU takes one member and no residual or x_sumsq");
+  }
+  const GemvPrologueArgs pro{prologue == EXL3_PROLOGUE_RMSNORM ? kProNorm : kProSwiglu,
+                             x, residual, residual_out, w, suh, eps, x_sumsq, y_residual, y_sumsq};
+  return gemv_run(nullptr, pro, trellis, n_members, member_n, k, K, cb, svh, bias, y, out_dtype, rows, flags,
+                  workspace, workspace_bytes, 0, stream);
 }
 
 extern "C" int exl3_gemv(const uint16_t* xh, const uint32_t* const* trellis, int n_members, const int* member_n,

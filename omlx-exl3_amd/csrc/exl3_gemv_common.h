@@ -20,7 +20,21 @@ struct GemvArgs {
   float* partials;
   uint32_t* counters;
   int k, KT, rows, n_total, S, kt_per_split;
+  // input prologue (kProNone: xh is the rotated input)
+  int pro;
+  const uint16_t* px;         // kProNorm: x (rows, k); kProSwiglu: gate | up (rows, 2k)
+  const uint16_t* pres;       // kProNorm: residual (rows, k) or null
+  uint16_t* pres_out;         // kProNorm: h = x + residual (rows, k) or null
+  const uint16_t* pw;         // kProNorm: RMSNorm weight (k)
+  float eps;
+  const uint16_t* psuh;       // input signs (n_members, k)
+  const double* pss;          // kProNorm without residual: sums of squares of x per 128-block (rows, k/128)
+  // output epilogue (fp16 output): y = fp16(y + eres), and per-128-block sums of squares of y to ess
+  const uint16_t* eres;       // (rows, n_total) or null
+  double* ess;                // (rows, n_total / 128) or null
 };
+
+enum Prologue : int { kProNone = 0, kProNorm = 1, kProSwiglu = 2 };
 
 constexpr int kMaxRows = 16;
 constexpr int kBufferFlags = 0x00020000;   // raw buffer descriptor word 3 (32-bit data, no swizzle) for gfx950

@@ -13,53 +13,6 @@
 
 namespace exl3 {
 
-template <int DT>
-__device__ __forceinline__ void load8(const void* base, size_t i0, float (&v)[8]) {
-  if constexpr (DT == kF32) {
-    const f32x4* p = reinterpret_cast<const f32x4*>(static_cast<const float*>(base) + i0);
-    const f32x4 a = p[0], b = p[1];
-    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-  } else {
-    const u32x4 q = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(base) + i0);
-    const uint32_t d[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint16_t lo = (uint16_t)(d[j] & 0xFFFFu), hi = (uint16_t)(d[j] >> 16);
-      if constexpr (DT == kF16) {
-        v[2 * j] = f16_to_f32(lo);
-        v[2 * j + 1] = f16_to_f32(hi);
-      } else {
-        v[2 * j] = bf16_to_f32(lo);
-        v[2 * j + 1] = bf16_to_f32(hi);
-      }
-    }
-  }
-}
-
-template <int DT>
-__device__ __forceinline__ void store8(void* base, size_t i0, const float (&v)[8]) {
-  if constexpr (DT == kF32) {
-    f32x4* p = reinterpret_cast<f32x4*>(static_cast<float*>(base) + i0);
-    p[0] = f32x4{v[0], v[1], v[2], v[3]};
-    p[1] = f32x4{v[4], v[5], v[6], v[7]};
-  } else {
-    uint32_t d[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      uint16_t lo, hi;
-      if constexpr (DT == kF16) {
-        lo = f32_to_f16(v[2 * j]);
-        hi = f32_to_f16(v[2 * j + 1]);
-      } else {
-        lo = f32_to_bf16(v[2 * j]);
-        hi = f32_to_bf16(v[2 * j + 1]);
-      }
-      d[j] = (uint32_t)lo | ((uint32_t)hi << 16);
-    }
-    *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(base) + i0) = u32x4{d[0], d[1], d[2], d[3]};
-  }
-}
-
 // rotate the 8 values of this lane (element offset c0 within the row) for every member and store to xh
 __device__ __forceinline__ void rotate_members(const float (&xv)[8], const uint16_t* __restrict__ suh, int nm,
                                                int rows, int r, int k, size_t c0, uint16_t* __restrict__ xh,

@@ -8,7 +8,8 @@ launch per linear or sibling group on top of the producer's own kernel. For rows
   RMSNorm -> EXL3 consumers   input_layernorm -> q/k/v, post_attention_layernorm -> gate/up, the final
                               norm -> lm_head: one kernel writes the norm output (other readers still
                               get it) and every consumer's rotated input, grouped or not
-  SwiGLU -> down_proj         one kernel from the gate/up GEMV output to down_proj's rotated input
+  SwiGLU -> down_proj         down_proj's GEMV forms its rotated input from the gate/up GEMV output
+                              inside its own launch (no SwiGLU launch)
 
 Priming is keyed on the identity of the norm's output tensor: a consumer that receives any other tensor
 (a view, a cast) computes the rotation itself, so every call path stays correct. Modules keep their
@@ -24,7 +25,7 @@ from __future__ import annotations
 import torch
 from torch import nn
 
-from .kernels import MAX_GEMV_ROWS, norm_rot, swiglu_rot
+from .kernels import MAX_GEMV_ROWS, norm_rot
 from .linear import EXL3Linear
 
 _fused_classes: dict = {}
@@ -83,8 +84,7 @@ def _fused_mlp_class(base):
                 if rows > MAX_GEMV_ROWS or not ENABLED:
                     return base.forward(self, x)
                 gu = self.gate_proj._group.gemv(x, torch.float16)       # (rows, 2 * hidden): [gate | up]
-                xh = swiglu_rot(gu, self.down_proj._suh)
-                y = self.down_proj.gemv_rotated(xh, x.dtype)
+                y = self.down_proj.gemv_swiglu(gu, x.dtype)
                 return y.reshape(x.shape[:-1] + (y.shape[-1],))
 
         FusedMLP.__name__ = FusedMLP.__qualname__ = base.__name__

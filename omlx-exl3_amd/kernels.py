@@ -16,6 +16,7 @@ import torch
 
 from ._capi import DTYPE_CODE, Exl3Error, check, lib, ptr, stream_handle
 
+PROLOGUE_NONE, PROLOGUE_RMSNORM, PROLOGUE_SWIGLU = 0, 1, 2      # exl3_gemv_fused input prologues
 MAX_GEMV_ROWS = 8           # rows at or below which EXL3Linear takes the GEMV path (kernels.py:260)
 GEMV_ROWS_LIMIT = 16        # rows one GEMV launch accepts
 GEMV_EXACT, GEMV_FAST, GEMV_TABLE = 0, 1, 2
@@ -159,12 +160,7 @@ class TrellisGemvPlan:
         self._tr_key = None
         self._tr_c = None
 
-    def __call__(self, xh: torch.Tensor, trellises: list[torch.Tensor], bias: torch.Tensor | None = None,
-                 out: torch.Tensor | None = None) -> torch.Tensor:
-        """trellises: one per member. Returns (rows, n) in out_dtype."""
-        _dev(xh, "xh")
-        _require(xh.dtype == torch.float16 and xh.numel() == self.nsub * self.rows * self.k,
-                 f"xh must be fp16 ({self.nsub}, {self.rows}, {self.k})")
+    def _bind(self, trellises: list[torch.Tensor], bias: torch.Tensor | None, out: torch.Tensor | None, device):
         _require(len(trellises) == self.nsub, "one trellis per member")
         key = tuple(t.data_ptr() for t in trellises)
         if key != self._tr_key:
@@ -177,13 +173,67 @@ class TrellisGemvPlan:
             _require(bias.dtype == self.out_dtype and bias.numel() == self.n and bias.is_contiguous(),
                      "bias must be contiguous, out_dtype, n elements")
         if out is None:
-            out = torch.empty((self.rows, self.n), dtype=self.out_dtype, device=xh.device)
+            out = torch.empty((self.rows, self.n), dtype=self.out_dtype, device=device)
+        return out
+
+    def __call__(self, xh: torch.Tensor, trellises: list[torch.Tensor], bias: torch.Tensor | None = None,
+                 out: torch.Tensor | None = None) -> torch.Tensor:
+        """trellises: one per member. Returns (rows, n) in out_dtype."""
+        _dev(xh, "xh")
+        _require(xh.dtype == torch.float16 and xh.numel() == self.nsub * self.rows * self.k,
+                 f"xh must be fp16 ({self.nsub}, {self.rows}, {self.k})")
+        out = self._bind(trellises, bias, out, xh.device)
         rc = lib().exl3_gemv_ex(ptr(xh), self._tr_c, self.nsub, self._ns_c, self.k, self.K, self.cb, ptr(self.svh),
                                 ptr(bias), ptr(out), DTYPE_CODE[self.out_dtype], self.rows, self.flags,
                                 ptr(self.workspace), self.workspace.numel(), self.kt_per_split,
                                 stream_handle(xh.device))
         check(rc, "exl3_gemv")
         return out
+
+    def fused(self, prologue: int, x: torch.Tensor, trellises: list[torch.Tensor], *,
+              residual: torch.Tensor | None = None, residual_out: torch.Tensor | None = None,
+              weight: torch.Tensor | None = None, eps: float = 0.0, x_sumsq: torch.Tensor | None = None,
+              suh: torch.Tensor | None = None, bias: torch.Tensor | None = None,
+              y_residual: torch.Tensor | None = None, y_sumsq: torch.Tensor | None = None,
+              out: torch.Tensor | None = None) -> torch.Tensor:
+        """The GEMV with its neighbouring element-wise steps in the same launch (exl3_gemv_fused).
+        prologue PROLOGUE_NONE: x is the rotated input (n_members, rows, k); PROLOGUE_RMSNORM: x (rows, k)
+        [+ residual, h to residual_out], RMSNorm with weight / eps (x_sumsq: the block sums of squares of x
+        from a previous call, no residual), rotations by suh (n_members, k); PROLOGUE_SWIGLU: x = [gate | up]
+        (rows, 2k), suh (k). Epilogue (fp16 output): y += y_residual; y_sumsq (rows, n/128) fp64 receives
+        the block sums of squares of y."""
+        _dev(x, "x")
+        _require(x.dtype == torch.float16 and x.is_contiguous(), "x must be contiguous fp16")
+        want = {PROLOGUE_NONE: self.nsub * self.rows * self.k, PROLOGUE_RMSNORM: self.rows * self.k,
+                PROLOGUE_SWIGLU: 2 * self.rows * self.k}.get(prologue)
+        _require(want is not None and x.numel() == want, f"x has {x.numel()} elements, prologue {prologue} wants {want}")
+        for t, name, n, dt in ((residual, "residual", self.rows * self.k, torch.float16),
+                               (residual_out, "residual_out", self.rows * self.k, torch.float16),
+                               (weight, "weight", self.k, torch.float16),
+                               (x_sumsq, "x_sumsq", self.rows * (self.k // 128), torch.float64),
+                               (suh, "suh", (1 if prologue == PROLOGUE_SWIGLU else self.nsub) * self.k, torch.float16),
+                               (y_residual, "y_residual", self.rows * self.n, torch.float16),
+                               (y_sumsq, "y_sumsq", self.rows * (self.n // 128), torch.float64)):
+            if t is not None:
+                _dev(t, name)
+                _require(t.dtype == dt and t.is_contiguous() and t.numel() == n, f"{name}: contiguous {dt}, {n} elements")
+        out = self._bind(trellises, bias, out, x.device)
+        rc = lib().exl3_gemv_fused(prologue, ptr(x), ptr(residual), ptr(residual_out), ptr(weight), float(eps),
+                                   ptr(x_sumsq), ptr(suh), self._tr_c, self.nsub, self._ns_c, self.k, self.K, self.cb,
+                                   ptr(self.svh), ptr(bias), ptr(out), DTYPE_CODE[self.out_dtype], self.rows,
+                                   self.flags, ptr(y_residual), ptr(y_sumsq), ptr(self.workspace),
+                                   self.workspace.numel(), stream_handle(x.device))
+        check(rc, "exl3_gemv_fused")
+        return out
+
+    def rmsnorm(self, x: torch.Tensor, residual: torch.Tensor | None, weight: torch.Tensor, eps: float,
+                suh: torch.Tensor, trellises: list[torch.Tensor], **kw) -> torch.Tensor:
+        """fused(PROLOGUE_RMSNORM, ...): the GEMV of rot(rmsnorm(x + residual) * weight, suh_m) per member."""
+        return self.fused(PROLOGUE_RMSNORM, x, trellises, residual=residual, weight=weight, eps=eps, suh=suh, **kw)
+
+    def swiglu(self, gu: torch.Tensor, suh: torch.Tensor, trellises: list[torch.Tensor], **kw) -> torch.Tensor:
+        """fused(PROLOGUE_SWIGLU, ...): the GEMV of rot(silu(gate) * up, suh) with gu = [gate | up]."""
+        return self.fused(PROLOGUE_SWIGLU, gu, trellises, suh=suh, **kw)
 
 
 def prefill_gemm(xh: torch.Tensor, trellis: torch.Tensor, k: int, n: int, K: int, cb: int, svh: torch.Tensor,

@@ -25,7 +25,7 @@ import math
 import torch
 from torch import nn
 
-from .kernels import MAX_GEMV_ROWS, TrellisGemvPlan, prefill_gemm, rot
+from .kernels import MAX_GEMV_ROWS, PROLOGUE_NONE, TrellisGemvPlan, prefill_gemm, rot
 
 _HAD_SCALE = 1.0 / math.sqrt(128.0)
 EXL3_PARTS = ("trellis", "suh", "svh", "su", "sv", "mul1", "mcg", "bias")
@@ -154,16 +154,47 @@ class EXL3Linear(nn.Module):
             b = self._bias_cast[dtype] = self.bias.reshape(-1).to(dtype).contiguous()
         return b
 
-    def gemv_rotated(self, xh: torch.Tensor, out_dtype: torch.dtype, bias: torch.Tensor | None = None) -> torch.Tensor:
-        """(rows, out_features) from an already rotated input xh, (1, rows, k) or (rows, k)
-        (linear.py:84-92). `bias` (out_dtype, out_features) is added inside the kernel before rounding."""
+    def _plan(self, rows: int, out_dtype: torch.dtype) -> TrellisGemvPlan:
         self._prepare()
-        rows = xh.shape[-2]
         plan = self._plans.get((rows, out_dtype))
         if plan is None:
             plan = self._plans[(rows, out_dtype)] = TrellisGemvPlan(
                 self.in_features, [self.out_features], self._K, self._cb, self._svh, rows, out_dtype)
-        return plan(xh.contiguous(), [self._tr], bias=bias)
+        return plan
+
+    def gemv_rotated(self, xh: torch.Tensor, out_dtype: torch.dtype, bias: torch.Tensor | None = None,
+                     y_residual: torch.Tensor | None = None, y_sumsq: torch.Tensor | None = None) -> torch.Tensor:
+        """(rows, out_features) from an already rotated input xh, (1, rows, k) or (rows, k)
+        (linear.py:84-92). `bias` (out_dtype, out_features) is added inside the kernel before rounding.
+        Epilogue (fp16): y_residual is added to the output and y_sumsq (rows, out_features / 128) fp64
+        receives its block sums of squares, for a following gemv_rmsnorm."""
+        plan = self._plan(xh.shape[-2], out_dtype)
+        if y_residual is None and y_sumsq is None:
+            return plan(xh.contiguous(), [self._tr], bias=bias)
+        return plan.fused(PROLOGUE_NONE, xh.contiguous(), [self._tr], bias=bias, y_residual=y_residual,
+                          y_sumsq=y_sumsq)
+
+    def gemv_rmsnorm(self, x: torch.Tensor, residual: torch.Tensor | None, weight: torch.Tensor, eps: float,
+                     out_dtype: torch.dtype, residual_out: torch.Tensor | None = None,
+                     x_sumsq: torch.Tensor | None = None) -> torch.Tensor:
+        """(rows, out_features) of this linear applied to rmsnorm(x + residual) * weight, with the residual
+        add, norm and input rotation inside the GEMV launch; h = x + residual is written to residual_out
+        when given; x_sumsq: x's block sums of squares from the producing launch (no residual). fp16 x,
+        residual, weight; rows <= MAX_GEMV_ROWS. Equal, bit for bit, to norm_rot followed by gemv_rotated."""
+        rows = x.numel() // self.in_features
+        return self._plan(rows, out_dtype).rmsnorm(x, residual, weight, eps, self._suh2d, [self._tr],
+                                                   bias=self._bias_for(out_dtype), residual_out=residual_out,
+                                                   x_sumsq=x_sumsq)
+
+    def gemv_swiglu(self, gu: torch.Tensor, out_dtype: torch.dtype, y_residual: torch.Tensor | None = None,
+                    y_sumsq: torch.Tensor | None = None) -> torch.Tensor:
+        """(rows, out_features) of this linear applied to silu(gate) * up for gu = [gate | up]
+        (rows, 2 * in_features) fp16, the SwiGLU and input rotation inside the GEMV launch (epilogue as
+        gemv_rotated). Equal, bit for bit, to swiglu_rot followed by gemv_rotated."""
+        rows = gu.numel() // (2 * self.in_features)
+        return self._plan(rows, out_dtype).swiglu(gu.contiguous(), self._suh, [self._tr],
+                                                  bias=self._bias_for(out_dtype), y_residual=y_residual,
+                                                  y_sumsq=y_sumsq)
 
     def _prefill(self, xh: torch.Tensor, out_dtype: torch.dtype, bias: torch.Tensor | None) -> torch.Tensor:
         """had128(xh @ W_inner) * svh (+ bias) for many rows (linear.py:97-105), one fused launch."""
@@ -231,17 +262,31 @@ class EXL3SiblingGroup:
         """The next call with exactly this tensor uses xh (n_members, rows, k) as its rotated input."""
         self._primed = (x, xh)
 
+    def _plan(self, rows: int, out_dtype: torch.dtype) -> TrellisGemvPlan:
+        plan = self.plans.get((rows, out_dtype))
+        if plan is None:
+            plan = self.plans[(rows, out_dtype)] = TrellisGemvPlan(self.k, self.ns, self.K, self.cb, self.svh,
+                                                                   rows, out_dtype)
+        return plan
+
     def gemv(self, x: torch.Tensor, out_dtype: torch.dtype) -> torch.Tensor:
         """All members' outputs, concatenated: (rows, sum(ns)) in out_dtype (rows <= MAX_GEMV_ROWS)."""
         rows = x.numel() // self.k
         primed, self._primed = self._primed, None
         xh = primed[1] if primed is not None and primed[0] is x else \
             rot(x.reshape(rows, self.k).contiguous(), self.suh)
-        plan = self.plans.get((rows, out_dtype))
-        if plan is None:
-            plan = self.plans[(rows, out_dtype)] = TrellisGemvPlan(self.k, self.ns, self.K, self.cb, self.svh,
-                                                                   rows, out_dtype)
-        return plan(xh.contiguous(), self.trs)
+        return self._plan(rows, out_dtype)(xh.contiguous(), self.trs)
+
+    def gemv_rmsnorm(self, x: torch.Tensor, residual: torch.Tensor | None, weight: torch.Tensor, eps: float,
+                     out_dtype: torch.dtype, residual_out: torch.Tensor | None = None,
+                     x_sumsq: torch.Tensor | None = None) -> torch.Tensor:
+        """All members' outputs (rows, sum(ns)) for the input rmsnorm(x + residual) * weight, with the
+        residual add, norm and every member's rotation inside the one GEMV launch (h = x + residual to
+        residual_out when given; x_sumsq as EXL3Linear.gemv_rmsnorm). Equal, bit for bit, to norm_rot
+        followed by gemv."""
+        rows = x.numel() // self.k
+        return self._plan(rows, out_dtype).rmsnorm(x, residual, weight, eps, self.suh, self.trs,
+                                                   residual_out=residual_out, x_sumsq=x_sumsq)
 
     def __call__(self, x: torch.Tensor) -> tuple:
         if self._cache_x is x:
