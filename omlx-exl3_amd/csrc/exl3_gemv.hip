@@ -143,6 +143,100 @@ __device__ void stage_prologue(const GemvArgs& a, int m, int blk_in_member, int 
   }
 }
 
+// Early prologue operands of one thread for a single row: the 8 elements of the 128-block of its 16-lane
+// group (x or gate, w or up, suh) and one of the producer's block sums of squares. Loaded before the trellis
+// prefetch, so they do not wait behind it (a wavefront's loads complete in issue order).
+struct ProPre {
+  u32x4 x, w, s;
+  double ss;
+  bool valid;
+};
+
+// Early form of stage_prologue for one row with the sums of squares given (RMSNORM) or SwiGLU, when every
+// 128-block of the split has its own 16-lane group: issue the loads.
+__device__ __forceinline__ ProPre prologue_preload(const GemvArgs& a, int m, int kt0, int kt1) {
+  ProPre p{};
+  const int tid = threadIdx.x, lane = tid & 63, k = a.k;
+  const int b0 = kt0 >> 3, nb = ((kt1 + 7) >> 3) - b0;
+  p.valid = (tid >> 4) < nb;
+  if (p.valid) {
+    const int c0 = (b0 + (tid >> 4)) * 128 + (lane & 15) * 8;
+    p.x = *reinterpret_cast<const u32x4*>(a.px + c0);
+    p.w = *reinterpret_cast<const u32x4*>(a.pro == kProNorm ? a.pw + c0 : a.px + k + c0);
+    p.s = *reinterpret_cast<const u32x4*>(a.psuh + (size_t)m * k + c0);
+  }
+  if (a.pro == kProNorm && tid < k / 128) p.ss = a.pss[tid];
+  return p;
+}
+
+__device__ __forceinline__ void unpack8(const u32x4& q, float (&v)[8]) {
+  const uint32_t d[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    v[2 * j] = f16_to_f32((uint16_t)(d[j] & 0xFFFFu));
+    v[2 * j + 1] = f16_to_f32((uint16_t)(d[j] >> 16));
+  }
+}
+
+// The rest of the early prologue, after the trellis prefetch: the same values as stage_prologue.
+template <bool SPLIT>
+__device__ void prologue_finish(const GemvArgs& a, const ProPre& p, int kt0, int kt1, int nrec, u32x4* xs,
+                                double (*ss_part)[16], float* inv_rms) {
+  constexpr int RW = SPLIT ? 4 : 2;
+  const int tid = threadIdx.x, nthr = blockDim.x, lane = tid & 63, wave = tid >> 6, nw = nthr >> 6;
+  const int nkt = kt1 - kt0;
+  for (int idx = nkt * RW + tid; idx < (nrec + 1) * RW; idx += nthr) xs[idx] = u32x4{0u, 0u, 0u, 0u};
+  if (a.pro == kProNorm) {
+    double ss = p.ss;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+    if (lane == 0) ss_part[0][wave] = ss;
+    __syncthreads();
+    if (tid == 0) {
+      double tot = 0.0;
+      for (int w = 0; w < nw; ++w) tot += ss_part[0][w];
+      const float mean = (float)tot / (float)a.k;
+      const float v = mean + a.eps;
+      inv_rms[0] = (float)(1.0 / sqrt((double)v));
+    }
+    __syncthreads();
+  }
+  if (!p.valid) return;
+  const int c0 = ((kt0 >> 3) + (tid >> 4)) * 128 + (lane & 15) * 8;
+  const int kt = c0 >> 4;
+  float v[8], w[8], s[8];
+  unpack8(p.x, v);
+  unpack8(p.w, w);
+  unpack8(p.s, s);
+  if (a.pro == kProNorm) {
+    const float inv = inv_rms[0];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = round_through<kF16>(w[i] * round_through<kF16>(v[i] * inv));
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float ex = (float)exp(-(double)v[i]);   // exp(-g) rounded once to fp32
+      v[i] = (v[i] / (1.0f + ex)) * w[i];
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = v[i] * s[i];
+  fwht128_lane8(v, lane);
+  if (kt >= kt0 && kt < kt1) {
+    uint32_t d[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      d[j] = (uint32_t)f32_to_f16(v[2 * j] * kHadScale) | ((uint32_t)f32_to_f16(v[2 * j + 1] * kHadScale) << 16);
+    const int rec = kt - kt0, half = (c0 >> 3) & 1;
+    if constexpr (SPLIT) {
+      xs[rec * 4 + 2 * half] = dup4(d[0], d[1]);
+      xs[rec * 4 + 2 * half + 1] = dup4(d[2], d[3]);
+    } else {
+      xs[rec * 2 + half] = u32x4{d[0], d[1], d[2], d[3]};
+    }
+  }
+}
+
 template <int K, int CB, int L, int OT>
 __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
   constexpr bool SPLIT = L == kSplit;
@@ -194,37 +288,61 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
     load_run<K>(rs_t, vo_t + adv, vo_wp + adv, 0u, st.w, st.wp);
   };
 
+  // ---- this split's activations for LDS: loads issued before the trellis prefetch ----
+  // record (kl, r) = the 16 activations of k-tile kt0 + kl for batch row r; WK extra iterations of zero
+  // records (read by the last phase's look-ahead) and a zero record for absent rows at the end
+  const int nrec = (iters + WK) * 4 * rows;
+  const int nunits = (nrec + 1) * RW;
+  const uint16_t* __restrict__ xh = a.xh + (size_t)m * rows * a.k;
+  auto load_unit = [&](int idx) {   // raw 16 (kPair) or 8 (kSplit) bytes of unit idx, zero outside
+    u32x4 v = {0u, 0u, 0u, 0u};
+    const int rec = idx / RW, h = idx % RW;
+    if (rec < nrec) {
+      const int kl = rec / rows, r = rec - kl * rows;
+      if (kl < nkt) {
+        const uint16_t* src = xh + (size_t)r * a.k + (size_t)(kt0 + kl) * 16;
+        if constexpr (SPLIT) {
+          const uint2 p = reinterpret_cast<const uint2*>(src)[h];   // activations 4h .. 4h+3
+          v.x = p.x;
+          v.y = p.y;
+        } else {
+          v = reinterpret_cast<const u32x4*>(src)[h];
+        }
+      }
+    }
+    return v;
+  };
+  auto put_unit = [&](int idx, const u32x4& v) {
+    if constexpr (SPLIT) xs[idx] = dup4(v.x, v.y);
+    else xs[idx] = v;
+  };
+  const int b_split = ((kt1 + 7) >> 3) - (kt0 >> 3);
+  const bool early_pro = a.pro != kProNone && rows == 1 && (a.pro == kProSwiglu || a.pss != nullptr) &&
+                         b_split <= (nthr >> 4) && a.k / 128 <= nthr;
+  ProPre pp{};
+  u32x4 pre0 = {0u, 0u, 0u, 0u}, pre1 = {0u, 0u, 0u, 0u};
+  if (early_pro) {
+    pp = prologue_preload(a, m, kt0, kt1);
+  } else if (a.pro == kProNone) {
+    if (tid < nunits) pre0 = load_unit(tid);
+    if (tid + nthr < nunits) pre1 = load_unit(tid + nthr);
+  }
+
   Stage<K> st[D];
   static_for<0, D>([&](auto P) {
     issue_it(st[decltype(P)::value], decltype(P)::value);
     __builtin_amdgcn_sched_barrier(0);
   });
 
-  // ---- stage this split's activations in LDS, zero past the split ----
-  // record (kl, r) = the 16 activations of k-tile kt0 + kl for batch row r; WK extra iterations of zero
-  // records (read by the last phase's look-ahead) and a zero record for absent rows at the end
-  const int nrec = (iters + WK) * 4 * rows;
-  if (a.pro != kProNone) {
+  // ---- stage them in LDS, zero past the split ----
+  if (early_pro) {
+    prologue_finish<SPLIT>(a, pp, kt0, kt1, nrec, xs, ss_part, inv_rms);
+  } else if (a.pro != kProNone) {
     stage_prologue<SPLIT>(a, m, blk - blk0, kt0, kt1, nrec, xs, ss_part, inv_rms);
   } else {
-    const uint16_t* __restrict__ xh = a.xh + (size_t)m * rows * a.k;
-    for (int idx = tid; idx < (nrec + 1) * RW; idx += nthr) {
-      const int rec = idx / RW, h = idx % RW;
-      u32x4 v = {0u, 0u, 0u, 0u};
-      if (rec < nrec) {
-        const int kl = rec / rows, r = rec - kl * rows;
-        if (kl < nkt) {
-          const uint16_t* src = xh + (size_t)r * a.k + (size_t)(kt0 + kl) * 16;
-          if constexpr (SPLIT) {
-            const uint2 p = reinterpret_cast<const uint2*>(src)[h];   // activations 4h .. 4h+3
-            v = dup4(p.x, p.y);
-          } else {
-            v = reinterpret_cast<const u32x4*>(src)[h];
-          }
-        }
-      }
-      xs[idx] = v;
-    }
+    if (tid < nunits) put_unit(tid, pre0);
+    if (tid + nthr < nunits) put_unit(tid + nthr, pre1);
+    for (int idx = tid + 2 * nthr; idx < nunits; idx += nthr) put_unit(idx, load_unit(idx));
   }
   __syncthreads();
 
