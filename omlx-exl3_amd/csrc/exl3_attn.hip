@@ -107,24 +107,29 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
     d = __builtin_amdgcn_fdot2(as_h2(w.w), as_h2(qp[3]), d, false);
     return sum16(d) * scale;
   };
+  // batches of kAttnUnroll positions per slot, every batch's loads issued together (the last one predicated)
+  constexpr int kBatch = kAttnUnroll * kAttnSlots;
   float lmax = -INFINITY;
-  int j = slot;
-  for (; j + (kAttnUnroll - 1) * kAttnSlots < L; j += kAttnUnroll * kAttnSlots) {
+  for (int j = slot; j < L; j += kBatch) {
     u32x4 w[kAttnUnroll];
 #pragma unroll
-    for (int u = 0; u < kAttnUnroll; ++u) w[u] = krow[(size_t)(j + u * kAttnSlots) * 16];
+    for (int u = 0; u < kAttnUnroll; ++u)
+      if (j + u * kAttnSlots < L) w[u] = krow[(size_t)(j + u * kAttnSlots) * 16];
 #pragma unroll
     for (int u = 0; u < kAttnUnroll; ++u) {
-      const float d = score(w[u]);
-      if (dg == 0) sp[j + u * kAttnSlots] = d;
-      lmax = fmaxf(lmax, d);
+      if (j + u * kAttnSlots < L) {
+        const float d = score(w[u]);
+        if (dg == 0) sp[j + u * kAttnSlots] = d;
+        lmax = fmaxf(lmax, d);
+      }
     }
   }
-  for (; j < L; j += kAttnSlots) {
-    const float d = score(krow[(size_t)j * 16]);
-    if (dg == 0) sp[j] = d;
-    lmax = fmaxf(lmax, d);
-  }
+  // the first batch of V rows, in flight during the softmax reductions
+  const u32x4* vrow = reinterpret_cast<const u32x4*>(vc + kv_row0 * kAttnHD) + dg;
+  u32x4 vw[kAttnUnroll];
+#pragma unroll
+  for (int u = 0; u < kAttnUnroll; ++u)
+    if (slot + u * kAttnSlots < L) vw[u] = vrow[(size_t)(slot + u * kAttnSlots) * 16];
   const float gmax = block_reduce(lmax, red, true);
   float lsum = 0.f;
   for (int jj = tid; jj < L; jj += kAttnThreads) {
@@ -136,7 +141,6 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
   const float inv = L > 0 ? 1.0f / gsum : 0.f;
 
   // ---- o = sum_j p_j v_j over this slot's positions, dimensions 8 dg .. 8 dg + 7 ----
-  const u32x4* vrow = reinterpret_cast<const u32x4*>(vc + kv_row0 * kAttnHD) + dg;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   auto accum = [&](const u32x4 w, float p) {
     const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
@@ -146,15 +150,16 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
       acc[2 * t + 1] += p * f16_to_f32((uint16_t)(ww[t] >> 16));
     }
   };
-  j = slot;
-  for (; j + (kAttnUnroll - 1) * kAttnSlots < L; j += kAttnUnroll * kAttnSlots) {
-    u32x4 w[kAttnUnroll];
+  for (int j = slot; j < L; j += kBatch) {
+    if (j != slot) {
 #pragma unroll
-    for (int u = 0; u < kAttnUnroll; ++u) w[u] = vrow[(size_t)(j + u * kAttnSlots) * 16];
+      for (int u = 0; u < kAttnUnroll; ++u)
+        if (j + u * kAttnSlots < L) vw[u] = vrow[(size_t)(j + u * kAttnSlots) * 16];
+    }
 #pragma unroll
-    for (int u = 0; u < kAttnUnroll; ++u) accum(w[u], sp[j + u * kAttnSlots] * inv);
+    for (int u = 0; u < kAttnUnroll; ++u)
+      if (j + u * kAttnSlots < L) accum(vw[u], sp[j + u * kAttnSlots] * inv);
   }
-  for (; j < L; j += kAttnSlots) accum(vrow[(size_t)j * 16], sp[j] * inv);
 #pragma unroll
   for (int i = 0; i < 8; ++i) so[slot][8 * dg + i] = acc[i];
   __syncthreads();

@@ -282,11 +282,14 @@ def _rope_ref(x, c, s):
     return (x * cc + rh * ss).half()
 
 
-@pytest.mark.parametrize("n_heads,n_kv,pos", [(48, 8, 37), (4, 2, 0), (8, 8, 255), (6, 1, 100)])
-def test_attn_decode_rotate_vs_torch(pk, n_heads, n_kv, pos):
+@pytest.mark.parametrize("n_heads,n_kv,pos,max_len", [(48, 8, 37, 256), (4, 2, 0, 256), (8, 8, 255, 256),
+                                                     (6, 1, 100, 256), (48, 8, 1500, 2048), (16, 2, 200, 256),
+                                                     (48, 8, 8191, 8192)])
+def test_attn_decode_rotate_vs_torch(pk, n_heads, n_kv, pos, max_len):
     """Decode attention kernel: cache append bit-exact vs the torch rope formulation, o within 2e-3 of an
-    fp32 torch attention, xh bit-exact vs the rotation kernel applied to o, other cache rows untouched."""
-    hd, max_len = 128, 256
+    fp32 torch attention, xh bit-exact vs the rotation kernel applied to o, other cache rows untouched,
+    a repeated call identical."""
+    hd = 128
     g = torch.Generator(device="cuda").manual_seed(pos + n_heads)
     q = torch.randn(n_heads * hd, device="cuda", generator=g).half()
     k = torch.randn(n_kv * hd, device="cuda", generator=g).half()
@@ -313,6 +316,8 @@ def test_attn_decode_rotate_vs_torch(pk, n_heads, n_kv, pos):
     e = ((o.float().view(-1) - ref).abs().max() / ref.abs().max()).item()
     assert e < 2e-3, e
     assert torch.equal(xh.view(1, -1), pk.kernels.rot(o, suh.view(1, -1)).view(1, -1))
+    xh2, o2 = pk.kernels.attn_decode_rotate(q, k, v, kc, vc, p, cos, sin, suh, want_o=True)
+    assert torch.equal(xh2, xh) and torch.equal(o2, o)
 
 
 def test_attn_decode_out_of_range_position_writes_nothing(pk):
