@@ -130,6 +130,89 @@ __device__ __forceinline__ uint32_t hash_pos(const uint32_t* w, uint32_t wp) {
 // 3INST / MCG: the two fp16 summands of the codebook value as one packed register (a in low, b in high)
 __device__ __forceinline__ uint32_t split_pair(uint32_t h) { return (h & kMask3) ^ kXor3; }
 
+// ------------------------------------------------------------------------------------------------
+// Two positions' decode chains in one asm block. The compiler cannot see inside inline asm, so it puts a
+// wait state (s_nop 0) between an asm statement that writes a VGPR and the next instruction that reads it;
+// a chain of one-instruction asm statements pays that after every step (~2 per weight). Here the chains of
+// two positions are interleaved inside one block, where no such wait is needed (none of the steps but the
+// final high-half add writes part of a register), so only the block's output pays it once.
+// ------------------------------------------------------------------------------------------------
+#define EXL3_MAD(d, s, sel) "v_mad_u32_u16 " d ", " s ", %[mlo], %[add]" sel "\n\t"
+#define EXL3_PK(d, s, sel) "v_pk_mad_u16 " d ", " s ", %[mhi], " d sel "\n\t"
+#define EXL3_BOP(d) "v_bitop3_b32 " d ", " d ", %[mask], %[xv] bitop3:0x6a\n\t"
+// operand selects of a state in the low half (L) or the high half (H) of its register
+#define EXL3_MAD_L ""
+#define EXL3_MAD_H " op_sel:[1,0,0,0]"
+#define EXL3_PK_L " op_sel_hi:[0,1,1]"
+#define EXL3_PK_H ""
+#define EXL3_HASH2(o0, o1, h0, h1)                                                                         \
+  EXL3_MAD(o0, "%[s0]", EXL3_MAD_##h0) EXL3_MAD(o1, "%[s1]", EXL3_MAD_##h1) EXL3_PK(o0, "%[s0]", EXL3_PK_##h0) \
+  EXL3_PK(o1, "%[s1]", EXL3_PK_##h1) EXL3_BOP(o0) EXL3_BOP(o1)
+#define EXL3_HASH_INPUTS                                                                                   \
+  [s0] "v"(src0), [s1] "v"(src1), [mlo] "s"(mlo), [mhi] "s"(mhi16), [add] "v"(add), [mask] "s"(mask_s),   \
+      [xv] "v"(xor_v)
+
+// 3INST / MCG: u_i = (hash(s_i) & mask) ^ xor for the states in the low (or high, HI0 / HI1) halves of
+// src0 and src1 — the fp16 summand pairs of two codebook values.
+template <int CB, bool HI0, bool HI1>
+__device__ __forceinline__ void summands2(uint32_t src0, uint32_t src1, uint32_t mask_s, uint32_t xor_v,
+                                          uint32_t& u0, uint32_t& u1) {
+  constexpr uint32_t mlo = Codebook<CB>::mul & 0xFFFFu;
+  constexpr uint32_t mhi16 = Codebook<CB>::mul & 0xFFFF0000u;
+  const uint32_t add = Codebook<CB>::add;
+#define EXL3_SUMMANDS2(h0, h1) \
+  asm(EXL3_HASH2("%[u0]", "%[u1]", h0, h1) : [u0] "=&v"(u0), [u1] "=&v"(u1) : EXL3_HASH_INPUTS)
+  if constexpr (HI0 && HI1) EXL3_SUMMANDS2(H, H);
+  else if constexpr (HI0) EXL3_SUMMANDS2(H, L);
+  else if constexpr (HI1) EXL3_SUMMANDS2(L, H);
+  else EXL3_SUMMANDS2(L, L);
+#undef EXL3_SUMMANDS2
+}
+
+// 3INST / MCG: fp16(a0 + b0) in the low half and fp16(a1 + b1) in the high half for two states (the
+// exact decode of two positions: the same values as sum_pairs(split_pair(hash16(s0)), split_pair(...))).
+template <int CB, bool HI0, bool HI1>
+__device__ __forceinline__ uint32_t values2(uint32_t src0, uint32_t src1, uint32_t mask_s, uint32_t xor_v) {
+  constexpr uint32_t mlo = Codebook<CB>::mul & 0xFFFFu;
+  constexpr uint32_t mhi16 = Codebook<CB>::mul & 0xFFFF0000u;
+  const uint32_t add = Codebook<CB>::add;
+  uint32_t d, t0, t1;
+#define EXL3_VALUES2(h0, h1)                                                                                 \
+  asm(EXL3_HASH2("%[t0]", "%[t1]", h0, h1)                                                                  \
+      "v_add_f16_sdwa %[d], %[t0], %[t0] dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1\n\t" \
+      "v_add_f16_sdwa %[d], %[t1], %[t1] dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_1" \
+      : [d] "=&v"(d), [t0] "=&v"(t0), [t1] "=&v"(t1)                                                       \
+      : EXL3_HASH_INPUTS)
+  if constexpr (HI0 && HI1) EXL3_VALUES2(H, H);
+  else if constexpr (HI0) EXL3_VALUES2(H, L);
+  else if constexpr (HI1) EXL3_VALUES2(L, H);
+  else EXL3_VALUES2(L, L);
+#undef EXL3_VALUES2
+  return d;
+}
+#undef EXL3_MAD
+#undef EXL3_PK
+#undef EXL3_BOP
+#undef EXL3_MAD_L
+#undef EXL3_MAD_H
+#undef EXL3_PK_L
+#undef EXL3_PK_H
+#undef EXL3_HASH2
+#undef EXL3_HASH_INPUTS
+
+// Positions P and P + 1 of a run (3INST / MCG): their summand pairs, or their packed fp16 values.
+template <int CB, int K, int P>
+__device__ __forceinline__ void summands_pos2(const uint32_t* w, uint32_t wp, uint32_t xor_v, uint32_t& u0,
+                                              uint32_t& u1) {
+  summands2<CB, Win<K, P>::at_hi, Win<K, P + 1>::at_hi>(window_src<K, P>(w, wp), window_src<K, P + 1>(w, wp), kMask3,
+                                                        xor_v, u0, u1);
+}
+template <int CB, int K, int P>
+__device__ __forceinline__ uint32_t values_pos2(const uint32_t* w, uint32_t wp, uint32_t xor_v) {
+  return values2<CB, Win<K, P>::at_hi, Win<K, P + 1>::at_hi>(window_src<K, P>(w, wp), window_src<K, P + 1>(w, wp),
+                                                             kMask3, xor_v);
+}
+
 // 3INST / MCG: fp16(a0 + b0) in the low half and fp16(a1 + b1) in the high half (one RNE rounding each)
 __device__ __forceinline__ uint32_t sum_pairs(uint32_t u0, uint32_t u1) {
   uint32_t d;

@@ -512,14 +512,23 @@ constexpr int kMaxKtPerSplit = 96;
 // staged activations: at most 26 iterations x 4 k-tiles x 16 rows x 64 B (+ zero record) = 104 KiB + 64 B
 constexpr size_t kMaxGemvSmem = 112 * 1024;
 
-// k-tiles per split. Measured on MI355X at K = 6 (27B shapes), the GEMV's time is flat within a few percent
-// for splits of 40-96 k-tiles and grows outside that range: shorter splits add partial sums and pipeline
-// fills, longer ones leave too few workgroups for narrow outputs. Wide outputs (>= 128 blocks of 128
-// columns, 1000+ workgroups at 48) take 48, narrow ones 96. The split depends only on the shape, never on
-// the row count, so each row is summed in the same order whatever the batch (row-exact results).
+// k-tiles per split, from the shape alone: the split never depends on the row count, so each row is summed
+// in the same order whatever the batch (row-exact results). Wide outputs (>= 128 blocks of 128 columns)
+// take 48 k-tiles: 1,000+ workgroups, several per CU, and measured at K = 6 (27B shapes) their time is flat
+// within a few percent for 40-96. Narrow outputs take as many splits as fill the chip's 256 CUs once
+// (at most 96 k-tiles each): the decode VALU work then spreads over every CU with none running two
+// workgroups. Measured at K = 6, rows 1: o_proj (40 blocks) 13.5 -> 12.0 us with 6 splits instead of 4,
+// q/k/v (64 blocks) 14.0 -> 13.1 us with 4 instead of 5 (5 puts two workgroups on a quarter of the CUs).
+constexpr int kSplitFillWorkgroups = 256;   // MI355X's CU count
 static int auto_kt_per_split(int KT, int blocks) {
-  int kps = blocks >= 128 ? 48 : kMaxKtPerSplit;
   const int ktr = (KT + 3) / 4 * 4;
+  int kps = 48;
+  if (blocks < 128) {
+    int S = kSplitFillWorkgroups / blocks;
+    const int s_min = (KT + kMaxKtPerSplit - 1) / kMaxKtPerSplit;
+    if (S < s_min) S = s_min;
+    kps = ((KT + S - 1) / S + 3) / 4 * 4;
+  }
   return kps > ktr ? ktr : kps;
 }
 

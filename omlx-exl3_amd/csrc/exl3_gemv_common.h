@@ -39,21 +39,15 @@ enum Prologue : int { kProNone = 0, kProNorm = 1, kProSwiglu = 2 };
 constexpr int kMaxRows = 16;
 constexpr int kBufferFlags = 0x00020000;   // raw buffer descriptor word 3 (32-bit data, no swizzle) for gfx950
 
-__device__ __forceinline__ uint32_t bitop_split(uint32_t h, uint32_t mask_s, uint32_t xor_v) {
-  uint32_t u;
-  asm("v_bitop3_b32 %0, %1, %2, %3 bitop3:0x6a" : "=v"(u) : "v"(h), "s"(mask_s), "v"(xor_v));   // (h & M) ^ X
-  return u;
-}
-
 // Decode one run (32 positions) of K words + the word before into MFMA B registers.
 //   SPLIT: b[p] = (a_p, b_p) fp16 summands, p = 0..31
 //   pair : b[p/2] = (w_p, w_{p+1}) fp16, p even, 16 registers
 template <int K, int CB, bool SPLIT>
 __device__ __forceinline__ void decode_run(const uint32_t* w, uint32_t wp, uint32_t* b, uint32_t xor_v) {
   if constexpr (SPLIT) {
-    static_for<0, 32>([&](auto P) {
-      constexpr int p = decltype(P)::value;
-      b[p] = bitop_split(hash_pos<CB, K, p>(w, wp), kMask3, xor_v);
+    static_for<0, 16>([&](auto P) {
+      constexpr int p = 2 * decltype(P)::value;
+      summands_pos2<CB, K, p>(w, wp, xor_v, b[p], b[p + 1]);
     });
   } else if constexpr (CB == 2) {
     static_for<0, 16>([&](auto P) {
@@ -63,8 +57,7 @@ __device__ __forceinline__ void decode_run(const uint32_t* w, uint32_t wp, uint3
   } else {
     static_for<0, 16>([&](auto P) {
       constexpr int p = 2 * decltype(P)::value;
-      b[p / 2] = sum_pairs(bitop_split(hash_pos<CB, K, p>(w, wp), kMask3, xor_v),
-                           bitop_split(hash_pos<CB, K, p + 1>(w, wp), kMask3, xor_v));
+      b[p / 2] = values_pos2<CB, K, p>(w, wp, xor_v);
     });
   }
 }

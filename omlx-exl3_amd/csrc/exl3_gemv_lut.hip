@@ -65,8 +65,7 @@ __device__ __forceinline__ void decode_run_lut(const uint32_t* w, uint32_t wp, u
     } else if constexpr (CB == 2) {
       b[i] = mul1_pair(mul1_r(hash_pos<CB, K, p>(w, wp)), mul1_r(hash_pos<CB, K, p + 1>(w, wp)));
     } else {
-      b[i] = sum_pairs(bitop_split(hash_pos<CB, K, p>(w, wp), kMask3, xor_v),
-                       bitop_split(hash_pos<CB, K, p + 1>(w, wp), kMask3, xor_v));
+      b[i] = values_pos2<CB, K, p>(w, wp, xor_v);
     }
   });
 }

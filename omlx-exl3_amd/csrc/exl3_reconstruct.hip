@@ -58,9 +58,11 @@ __global__ __launch_bounds__(256) void reconstruct_kernel(const uint32_t* __rest
   whi[1] = u32x4{hi[4], hi[5], hi[6], hi[7]};
 }
 
-// All 65,536 states through the GEMV's exact decode path (hash16 from either half of a register, then
-// the packed fp16 pair sum or the packed MUL1 fma). The unused half of each source register holds junk
-// bits, which the 16-bit hash operands must ignore.
+// All 65,536 states through the GEMV's decode paths, with each state in either half of a register: 3INST /
+// MCG by values2 (the exact path), cross-checked against summands2 (the summand pairs of the fast path)
+// summed the same way, which writes an fp16 NaN (never a codebook value) where they disagree; MUL1 by
+// hash16 and the packed fma. The unused half of each source register holds junk bits, which the 16-bit
+// hash operands must ignore.
 template <int CB, bool HI>
 __global__ __launch_bounds__(256) void codebook_kernel(uint16_t* __restrict__ out) {
   const uint32_t i = blockIdx.x * 256 + threadIdx.x;   // pair index, 0..32767
@@ -68,10 +70,15 @@ __global__ __launch_bounds__(256) void codebook_kernel(uint16_t* __restrict__ ou
   const uint32_t junk0 = (s0 * 0x9E3779B9u) >> 16, junk1 = (s1 * 0x85EBCA6Bu) >> 16;
   const uint32_t src0 = HI ? (s0 << 16) | junk0 : s0 | (junk0 << 16);
   const uint32_t src1 = HI ? (s1 << 16) | junk1 : s1 | (junk1 << 16);
-  const uint32_t h0 = hash16<CB, HI>(src0), h1 = hash16<CB, HI>(src1);
   uint32_t d;
-  if constexpr (CB == 2) d = mul1_pair(mul1_r(h0), mul1_r(h1));
-  else d = sum_pairs(split_pair(h0), split_pair(h1));
+  if constexpr (CB == 2) {
+    d = mul1_pair(mul1_r(hash16<CB, HI>(src0)), mul1_r(hash16<CB, HI>(src1)));
+  } else {
+    d = values2<CB, HI, HI>(src0, src1, kMask3, kXor3);
+    uint32_t u0, u1;
+    summands2<CB, HI, HI>(src0, src1, kMask3, kXor3, u0, u1);
+    if (sum_pairs(u0, u1) != d) d = 0xFFFFFFFFu;
+  }
   out[s0] = (uint16_t)(d & 0xFFFFu);
   out[s1] = (uint16_t)(d >> 16);
 }
