@@ -365,3 +365,18 @@ def test_gemv_table_kernel_vs_hash_kernel(pk, K, cb):
         if rows == 16:
             plan1 = pk.kernels.TrellisGemvPlan(k, ns, K, cb, dev(svh), 1, torch.float32, table=True)
             assert torch.equal(plan1(dev(xh[:, :1].copy()), [dev(t) for t in trs])[0], ys[0][0])
+
+
+@pytest.mark.parametrize("rows", [1, 4])
+def test_gemv_table_kernel_wide_shape(pk, rows):
+    """27B gate/up shape (5120 -> 2 x 17408, K = 6): the table kernel's shares run 21 steps and cross
+    column-group boundaries (two segments per share); its output matches the hashing kernel's."""
+    k, ns, K = 5120, [17408, 17408], 6
+    rng = np.random.default_rng(77 + rows)
+    trs = [dev(O.random_trellis(k, n, K, 900 + i).view(np.int16)) for i, n in enumerate(ns)]
+    svh = dev((rng.standard_normal(sum(ns)) / np.sqrt(k)).astype(np.float16))
+    xh = dev(rng.standard_normal((len(ns), rows, k)).astype(np.float16))
+    ys = [pk.kernels.TrellisGemvPlan(k, ns, K, 0, svh, rows, torch.float32, table=t)(xh, trs) for t in (True, False)]
+    assert O.max_abs_rel(ys[0].cpu().numpy(), ys[1].cpu().numpy()) < 1e-4
+    again = pk.kernels.TrellisGemvPlan(k, ns, K, 0, svh, rows, torch.float32, table=True)(xh, trs)
+    assert torch.equal(again, ys[0])
