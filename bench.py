@@ -218,32 +218,40 @@ def mixed_k_benchmark(pk, torch, dev, rows_list=(1, 2, 4, 8), n_layers=8, reps=4
 
 def prefill_benchmark(pk, torch, dev, rows=4608, reps=3) -> dict:
     """Config 4: M = 4608 rotated fp16 activations through gate / up (5120 -> 17408) and down (17408 -> 5120)
-    at K = 6, each one fused launch (trellis tiles reconstructed in LDS, MFMA, Hadamard epilogue).
+    at K = 6. Both prefill forms are timed: "fused" (trellis tiles reconstructed in LDS, MFMA, Hadamard
+    epilogue, one launch) and "library" (W_inner^T reconstructed once, hipBLASLt fp16 GEMM, output rotation);
+    the headline figures are those of the form prefill_gemm picks at this row count ("auto").
     TFLOP/s = 2 M k n / time, against the 2.5 PFLOP/s dense fp16 MFMA peak."""
     g = torch.Generator(device=dev).manual_seed(5)
-    res, tot_flop, tot_ms = {}, 0.0, 0.0
+    per = {"fused": {}, "library": {}}
+    tot = {"fused": [0.0, 0.0], "library": [0.0, 0.0]}
     for name, k, n in (("gate", 5120, 17408), ("up", 5120, 17408), ("down", 17408, 5120)):
         tr = torch.randint(-32768, 32768, (k // 16, n // 16, 96), dtype=torch.int16, device=dev, generator=g)
         svh = torch.where(torch.rand(n, device=dev, generator=g) < 0.5, -1.0, 1.0).half()
         xh = torch.randn((rows, k), device=dev, generator=g).half()
         out = torch.empty((rows, n), dtype=torch.float16, device=dev)
-        pk.kernels.prefill_gemm(xh, tr, k, n, 6, 0, svh, out=out)
-        torch.cuda.synchronize()
-        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        s.record()
-        for _ in range(reps):
-            pk.kernels.prefill_gemm(xh, tr, k, n, 6, 0, svh, out=out)
-        e.record()
-        torch.cuda.synchronize()
-        ms = s.elapsed_time(e) / reps
-        flop = 2.0 * rows * k * n
-        res[name] = {"ms": round(ms, 3), "TFLOP_s": round(flop / ms / 1e9, 1)}
-        tot_flop += flop
-        tot_ms += ms
+        for path in ("fused", "library"):
+            pk.kernels.prefill_gemm(xh, tr, k, n, 6, 0, svh, out=out, path=path)
+            torch.cuda.synchronize()
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record()
+            for _ in range(reps):
+                pk.kernels.prefill_gemm(xh, tr, k, n, 6, 0, svh, out=out, path=path)
+            e.record()
+            torch.cuda.synchronize()
+            ms = s.elapsed_time(e) / reps
+            flop = 2.0 * rows * k * n
+            per[path][name] = {"ms": round(ms, 3), "TFLOP_s": round(flop / ms / 1e9, 1)}
+            tot[path][0] += flop
+            tot[path][1] += ms
         del tr, xh, out
-    tf = tot_flop / tot_ms / 1e9
-    return {"rows": rows, "per_proj": res, "TFLOP_s": round(tf, 1), "peak_TFLOP_s": MFMA_F16_PEAK_TFLOPS,
-            "mfma_frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4), "ms_total": round(tot_ms, 2)}
+    auto = "library" if rows >= pk.kernels.PREFILL_LIBRARY_ROWS else "fused"
+    tf = {p: tot[p][0] / tot[p][1] / 1e9 for p in tot}
+    return {"rows": rows, "path": auto, "per_proj": per[auto], "TFLOP_s": round(tf[auto], 1),
+            "peak_TFLOP_s": MFMA_F16_PEAK_TFLOPS, "mfma_frac": round(tf[auto] / MFMA_F16_PEAK_TFLOPS, 4),
+            "ms_total": round(tot[auto][1], 2),
+            "by_path": {p: {"TFLOP_s": round(tf[p], 1), "ms_total": round(tot[p][1], 2), "per_proj": per[p]}
+                        for p in per}}
 
 
 def log(msg: str) -> None:

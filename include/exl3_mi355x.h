@@ -162,6 +162,16 @@ int exl3_swiglu_rotate(const uint16_t* gu, const uint16_t* suh, int rows, int n,
 int exl3_prefill_gemm(const uint16_t* xh, const uint32_t* trellis, int k, int n, int K, int cb,
                       const uint16_t* svh, const void* bias, void* y, int out_dtype, int rows, void* stream);
 
+/* Output rotation of the large-row prefill form, which is built as the reference's prefill is
+ * (linear.py:97-105): exl3_reconstruct writes W_inner^T (bit-exact fp16), the caller multiplies
+ * g = xh @ W_inner in fp16 with fp32 accumulation using its BLAS library (a plain library GEMM), and this
+ * entry point replaces the reference's hadamard_transform(g) * svh: y = fp16(H128(g)/sqrt(128) * svh)
+ * (+ bias) per 128-column block, in the output dtype.
+ *   g fp16 (rows, n), 16-byte aligned; svh fp16 [n]; bias NULL or [n] in out_dtype; y (rows, n) in out_dtype.
+ *   n % 128 == 0, rows >= 1. */
+int exl3_prefill_out_rotate(const uint16_t* g, int rows, int n, const uint16_t* svh, const void* bias, void* y,
+                            int out_dtype, void* stream);
+
 /* Batch-1 decode attention producing o_proj's rotated input. No counterpart in the reference, which
  * fuses rotations into the norm and SwiGLU producers (fusion.py:4-18) but rotates o_proj's input with a
  * separate rot launch (linear.py:113-116); this entry point applies the same fusion to the attention output

@@ -1,0 +1,65 @@
+// SPDX-License-Identifier: Apache-2.0
+// Output rotation of the large-row prefill form: y = had128(g) * svh (+ bias) for a (rows, n) fp16 product g.
+// The large-row prefill is built as the reference's prefill is (src/omlx/exl3/linear.py:97-105: decode_wt to
+// fp16 weights, an fp16 matmul, hadamard_transform, svh): exl3_reconstruct writes W_inner^T once, the host
+// multiplies with the process's BLAS library (hipBLASLt through PyTorch: a plain library GEMM; linking this
+// library against the system hipBLASLt would bind it, by soname, to the different hipBLASLt build PyTorch has
+// already loaded), and this kernel applies the 128-point Hadamard transform of each 128-column block,
+// 1/sqrt(128), svh and bias. The fused kernel (exl3_prefill.hip) decodes every weight once per 256-row tile
+// and cannot overlap that VALU work with its MFMA work; at thousands of rows the decode-once form is faster,
+// at a few hundred the fused one is.
+#include "exl3_capi_common.h"
+#include "exl3_device.h"
+
+namespace exl3 {
+
+// One (row, block) per 16 lanes: lane l holds elements 8 l .. 8 l + 7 of the block.
+template <int OT>
+__global__ __launch_bounds__(256) void out_rotate_kernel(const uint16_t* __restrict__ g, int n, int groups,
+                                                         const uint16_t* __restrict__ svh,
+                                                         const void* __restrict__ bias, void* __restrict__ y) {
+  const int grp = blockIdx.x * 16 + (threadIdx.x >> 4);
+  if (grp >= groups) return;   // whole 16-lane groups leave together: the transform's shuffles stay inside one
+  const int nb = n / 128;
+  const int r = grp / nb, b = grp - r * nb;
+  const int lane = threadIdx.x & 63;
+  const int c0 = b * 128 + 8 * (lane & 15);
+  const u32x4 raw = *reinterpret_cast<const u32x4*>(g + (size_t)r * n + c0);
+  const uint32_t ww[4] = {raw.x, raw.y, raw.z, raw.w};
+  float e[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    e[2 * i] = f16_to_f32((uint16_t)(ww[i] & 0xFFFFu));
+    e[2 * i + 1] = f16_to_f32((uint16_t)(ww[i] >> 16));
+  }
+  fwht128_lane8(e, lane);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    float o = round_through<OT>(e[i] * kHadScale * f16_to_f32(svh[c0 + i]));
+    if (bias) o = o + load_as_f32<OT>(bias, c0 + i);
+    store_from_f32<OT>(y, (size_t)r * n + c0 + i, o);
+  }
+}
+
+}  // namespace exl3
+
+using namespace exl3;
+
+extern "C" int exl3_prefill_out_rotate(const uint16_t* g, int rows, int n, const uint16_t* svh, const void* bias,
+                                       void* y, int out_dtype, void* stream) {
+  EXL3_REQUIRE(g && svh && y, EXL3_ERR_ARG, "exl3_prefill_out_rotate: NULL pointer argument");
+  EXL3_REQUIRE(n > 0 && n % 128 == 0, EXL3_ERR_ARG, "exl3_prefill_out_rotate: n must be a positive multiple of 128");
+  EXL3_REQUIRE(rows >= 1 && (size_t)rows * (size_t)(n / 128) <= (size_t)INT32_MAX - 16, EXL3_ERR_ARG,
+               "exl3_prefill_out_rotate: rows must be 1 .. 2^31 / (n / 128)");
+  EXL3_REQUIRE(out_dtype >= 0 && out_dtype <= 2, EXL3_ERR_ARG, "exl3_prefill_out_rotate: bad out_dtype %d",
+               out_dtype);
+  EXL3_REQUIRE(aligned(g, 16), EXL3_ERR_ARG, "exl3_prefill_out_rotate: g must be 16-byte aligned");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int groups = rows * (n / 128);
+  const int grid = (groups + 15) / 16;
+  if (out_dtype == EXL3_DTYPE_F16) out_rotate_kernel<kF16><<<grid, 256, 0, st>>>(g, n, groups, svh, bias, y);
+  else if (out_dtype == EXL3_DTYPE_BF16) out_rotate_kernel<kBF16><<<grid, 256, 0, st>>>(g, n, groups, svh, bias, y);
+  else out_rotate_kernel<kF32><<<grid, 256, 0, st>>>(g, n, groups, svh, bias, y);
+  EXL3_LAUNCH_CHECK("exl3_prefill_out_rotate");
+  return EXL3_OK;
+}

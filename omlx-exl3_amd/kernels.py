@@ -236,18 +236,35 @@ class TrellisGemvPlan:
         return self.fused(PROLOGUE_SWIGLU, gu, trellises, suh=suh, **kw)
 
 
+# Row count from which prefill_gemm's "auto" path takes the library-GEMM form (exl3_prefill_gemm_lib)
+# instead of the fused reconstruct-in-LDS kernel (exl3_prefill_gemm).
+PREFILL_LIBRARY_ROWS = 1024
+
+
 def prefill_gemm(xh: torch.Tensor, trellis: torch.Tensor, k: int, n: int, K: int, cb: int, svh: torch.Tensor,
                  bias: torch.Tensor | None = None, out_dtype: torch.dtype = torch.float16,
-                 out: torch.Tensor | None = None) -> torch.Tensor:
-    """had128(xh @ W_inner) * svh (+ bias) for xh (rows, k) fp16 (already rotated), weights reconstructed
-    in LDS and contracted on MFMA (the fused form of linear.py:97-105)."""
+                 out: torch.Tensor | None = None, path: str = "auto") -> torch.Tensor:
+    """had128(xh @ W_inner) * svh (+ bias) for xh (rows, k) fp16 (already rotated) (linear.py:97-105).
+    path "fused": weights reconstructed in LDS and contracted on MFMA in one launch (exl3_prefill_gemm);
+    "library": the reference's structure - W_inner^T reconstructed once (exl3_reconstruct), an fp16 GEMM with
+    fp32 accumulation by the process's BLAS library (hipBLASLt through torch.matmul), then the output rotation
+    (exl3_prefill_out_rotate); "auto": the library form from PREFILL_LIBRARY_ROWS rows."""
     _dev(xh, "xh")
     rows = xh.numel() // k
     _require(xh.dtype == torch.float16 and xh.numel() == rows * k, "xh must be fp16 (rows, k)")
+    _require(path in ("auto", "fused", "library"), f"prefill_gemm: unknown path {path!r}")
     trellis_words(trellis, k, n, K)
     svh = svh.to(torch.float16).reshape(-1).contiguous()
     if out is None:
         out = torch.empty((rows, n), dtype=out_dtype, device=xh.device)
+    if path == "library" or (path == "auto" and rows >= PREFILL_LIBRARY_ROWS):
+        wt = torch.empty((n, k), dtype=torch.float16, device=xh.device)
+        check(lib().exl3_reconstruct(ptr(trellis), k, n, K, cb, 0, n // 16, ptr(wt), stream_handle(xh.device)),
+              "exl3_reconstruct")
+        g = torch.matmul(xh.reshape(rows, k), wt.t())
+        check(lib().exl3_prefill_out_rotate(ptr(g), rows, n, ptr(svh), ptr(bias), ptr(out), DTYPE_CODE[out_dtype],
+                                            stream_handle(xh.device)), "exl3_prefill_out_rotate")
+        return out
     check(lib().exl3_prefill_gemm(ptr(xh), ptr(trellis), k, n, K, cb, ptr(svh), ptr(bias), ptr(out),
                                   DTYPE_CODE[out_dtype], rows, stream_handle(xh.device)), "exl3_prefill_gemm")
     return out

@@ -248,8 +248,9 @@ def test_gemv_bias_and_split_override(pk):
 
 
 # ------------------------------------------------------------------------------------------ prefill
+@pytest.mark.parametrize("path", ["fused", "library"])
 @pytest.mark.parametrize("K,cb", [(6, 0), (4, 1), (3, 2), (8, 0)])
-def test_prefill_vs_oracle(pk, K, cb):
+def test_prefill_vs_oracle(pk, K, cb, path):
     k, n, rows = 512, 384, 200
     rng = np.random.default_rng(K + cb)
     tr = O.random_trellis(k, n, K, 9)
@@ -257,20 +258,63 @@ def test_prefill_vs_oracle(pk, K, cb):
     xh = rng.standard_normal((rows, k)).astype(np.float16)
     ref = O.gemv_ref(xh, O.reconstruct_inner(tr, k, n, K, cb), svh)
     for dt, bar in ((torch.float16, 2e-3), (torch.float32, 2e-3), (torch.bfloat16, 1e-2)):
-        y = pk.kernels.prefill_gemm(dev(xh), dev(tr), k, n, K, cb, dev(svh), out_dtype=dt)
+        y = pk.kernels.prefill_gemm(dev(xh), dev(tr), k, n, K, cb, dev(svh), out_dtype=dt, path=path)
         assert O.max_abs_rel(y.float().cpu().numpy(), ref) < bar, (dt,)
 
 
-def test_prefill_27b_shape_vs_reconstruct(pk):
-    k, n, K, rows = 5120, 17408, 6, 512
+@pytest.mark.parametrize("path,rows", [("fused", 512), ("library", 512), ("library", 1100)])
+def test_prefill_27b_shape_vs_reconstruct(pk, path, rows):
+    k, n, K = 5120, 17408, 6
     g = torch.Generator(device="cuda").manual_seed(3)
     tr = torch.randint(-32768, 32768, (k // 16, n // 16, 16 * K), dtype=torch.int16, device="cuda", generator=g)
     svh = (torch.randn(n, device="cuda", generator=g) * 0.01).half()
     xh = torch.randn((rows, k), device="cuda", generator=g).half()
     W = pk.kernels.decode_wt(tr, k, n, K, 0).float()
     ref = _had128_t(xh.float() @ W.T) * svh.float()
-    y = pk.kernels.prefill_gemm(xh, tr, k, n, K, 0, svh, out_dtype=torch.float32)
+    y = pk.kernels.prefill_gemm(xh, tr, k, n, K, 0, svh, out_dtype=torch.float32, path=path)
     assert ((y - ref).abs().max() / ref.abs().max()).item() < 2e-3
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16, torch.float32])
+def test_prefill_library_path_matches_fused_with_bias(pk, dt):
+    """Both prefill forms with a bias and every output dtype, ragged row count (not a multiple of the GEMM
+    or rotation tiles): within the GEMM bar of each other; the library form is deterministic."""
+    k, n, K, rows = 1024, 640, 5, 777
+    rng = np.random.default_rng(21)
+    tr = dev(O.random_trellis(k, n, K, 31))
+    svh = dev((rng.standard_normal(n) * 0.02).astype(np.float16))
+    bias = dev(rng.standard_normal(n).astype(np.float32)).to(dt)
+    xh = dev(rng.standard_normal((rows, k)).astype(np.float16))
+    ys = [pk.kernels.prefill_gemm(xh, tr, k, n, K, 1, svh, bias=bias, out_dtype=dt, path=p) for p in ("fused", "library")]
+    bar = 1e-2 if dt == torch.bfloat16 else 2e-3
+    assert O.max_abs_rel(ys[1].float().cpu().numpy(), ys[0].float().cpu().numpy()) < bar
+    again = pk.kernels.prefill_gemm(xh, tr, k, n, K, 1, svh, bias=bias, out_dtype=dt, path="library")
+    assert torch.equal(again, ys[1])
+
+
+def test_prefill_out_rotate_vs_torch_and_rejects(pk):
+    """The output rotation alone: fp16(H128(g)/sqrt(128) * svh) per 128-column block, bit-exact against the
+    rotation written in torch (fp32 butterflies in the same stage order); bad shapes are refused."""
+    lib = pk._capi.lib()
+    rows, n = 37, 384
+    g = torch.randn((rows, n), device="cuda").half()
+    svh = torch.where(torch.rand(n, device="cuda") < 0.5, -1.0, 1.0).half()
+    y = torch.empty((rows, n), dtype=torch.float16, device="cuda")
+    rc = lib.exl3_prefill_out_rotate(g.data_ptr(), rows, n, svh.data_ptr(), None, y.data_ptr(), 0,
+                                     pk._capi.stream_handle(g.device))
+    assert rc == 0
+    x = g.float().reshape(rows, n // 128, 128)
+    h = 1
+    while h < 128:                      # butterflies (a + b, a - b) over stride h, h = 1, 2, ..., 64
+        v = x.reshape(rows, n // 128, 128 // (2 * h), 2, h)
+        x = torch.stack((v[:, :, :, 0] + v[:, :, :, 1], v[:, :, :, 0] - v[:, :, :, 1]), dim=3).reshape(rows, n // 128, 128)
+        h *= 2
+    scale = torch.tensor(0.08838834764831845, dtype=torch.float32, device="cuda")
+    ref = ((x.reshape(rows, n) * scale) * svh.float()).half()
+    assert torch.equal(y, ref)
+    rc = lib.exl3_prefill_out_rotate(g.data_ptr(), rows, 200, svh.data_ptr(), None, y.data_ptr(), 0,
+                                     pk._capi.stream_handle(g.device))
+    assert rc == -1 and b"multiple of 128" in lib.exl3_last_error()
 
 
 # ------------------------------------------------------------------------------------------ decode attention
