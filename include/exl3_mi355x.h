@@ -167,7 +167,8 @@ int exl3_prefill_gemm(const uint16_t* xh, const uint32_t* trellis, int k, int n,
  * g = xh @ W_inner in fp16 with fp32 accumulation using its BLAS library (a plain library GEMM), and this
  * entry point replaces the reference's hadamard_transform(g) * svh: y = fp16(H128(g)/sqrt(128) * svh)
  * (+ bias) per 128-column block, in the output dtype.
- *   g fp16 (rows, n), 16-byte aligned; svh fp16 [n]; bias NULL or [n] in out_dtype; y (rows, n) in out_dtype.
+ *   g fp16 (rows, n) and svh fp16 [n], 16-byte aligned; bias NULL or [n] in out_dtype; y (rows, n) in
+ *   out_dtype, 16-byte aligned (32 for fp32).
  *   n % 128 == 0, rows >= 1. */
 int exl3_prefill_out_rotate(const uint16_t* g, int rows, int n, const uint16_t* svh, const void* bias, void* y,
                             int out_dtype, void* stream);

@@ -13,7 +13,14 @@
 
 namespace exl3 {
 
-// One (row, block) per 16 lanes: lane l holds elements 8 l .. 8 l + 7 of the block.
+template <int OT>
+__device__ __forceinline__ uint16_t to_bits16(float v) {
+  if constexpr (OT == kF16) return f32_to_f16(v);
+  else return f32_to_bf16(v);
+}
+
+// One (row, block) per 16 lanes: lane l holds elements 8 l .. 8 l + 7 of the block, read and written as
+// 16-byte vectors (two for fp32 output).
 template <int OT>
 __global__ __launch_bounds__(256) void out_rotate_kernel(const uint16_t* __restrict__ g, int n, int groups,
                                                          const uint16_t* __restrict__ svh,
@@ -24,20 +31,36 @@ __global__ __launch_bounds__(256) void out_rotate_kernel(const uint16_t* __restr
   const int r = grp / nb, b = grp - r * nb;
   const int lane = threadIdx.x & 63;
   const int c0 = b * 128 + 8 * (lane & 15);
-  const u32x4 raw = *reinterpret_cast<const u32x4*>(g + (size_t)r * n + c0);
-  const uint32_t ww[4] = {raw.x, raw.y, raw.z, raw.w};
-  float e[8];
+  const size_t o0 = (size_t)r * n + c0;
+  const u32x4 raw = *reinterpret_cast<const u32x4*>(g + o0);
+  const u32x4 svr = *reinterpret_cast<const u32x4*>(svh + c0);
+  const uint32_t ww[4] = {raw.x, raw.y, raw.z, raw.w}, sw[4] = {svr.x, svr.y, svr.z, svr.w};
+  float e[8], sv[8];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     e[2 * i] = f16_to_f32((uint16_t)(ww[i] & 0xFFFFu));
     e[2 * i + 1] = f16_to_f32((uint16_t)(ww[i] >> 16));
+    sv[2 * i] = f16_to_f32((uint16_t)(sw[i] & 0xFFFFu));
+    sv[2 * i + 1] = f16_to_f32((uint16_t)(sw[i] >> 16));
   }
   fwht128_lane8(e, lane);
+  float o[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    float o = round_through<OT>(e[i] * kHadScale * f16_to_f32(svh[c0 + i]));
-    if (bias) o = o + load_as_f32<OT>(bias, c0 + i);
-    store_from_f32<OT>(y, (size_t)r * n + c0 + i, o);
+    o[i] = round_through<OT>(e[i] * kHadScale * sv[i]);
+    if (bias) o[i] = o[i] + load_as_f32<OT>(bias, c0 + i);
+  }
+  if constexpr (OT == kF32) {
+    float* yp = static_cast<float*>(y) + o0;
+    reinterpret_cast<f32x4*>(yp)[0] = f32x4{o[0], o[1], o[2], o[3]};
+    reinterpret_cast<f32x4*>(yp)[1] = f32x4{o[4], o[5], o[6], o[7]};
+  } else {
+    u32x4 pk;
+    pk.x = (uint32_t)to_bits16<OT>(o[0]) | ((uint32_t)to_bits16<OT>(o[1]) << 16);
+    pk.y = (uint32_t)to_bits16<OT>(o[2]) | ((uint32_t)to_bits16<OT>(o[3]) << 16);
+    pk.z = (uint32_t)to_bits16<OT>(o[4]) | ((uint32_t)to_bits16<OT>(o[5]) << 16);
+    pk.w = (uint32_t)to_bits16<OT>(o[6]) | ((uint32_t)to_bits16<OT>(o[7]) << 16);
+    *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(y) + o0) = pk;
   }
 }
 
@@ -53,7 +76,8 @@ extern "C" int exl3_prefill_out_rotate(const uint16_t* g, int rows, int n, const
                "exl3_prefill_out_rotate: rows must be 1 .. 2^31 / (n / 128)");
   EXL3_REQUIRE(out_dtype >= 0 && out_dtype <= 2, EXL3_ERR_ARG, "exl3_prefill_out_rotate: bad out_dtype %d",
                out_dtype);
-  EXL3_REQUIRE(aligned(g, 16), EXL3_ERR_ARG, "exl3_prefill_out_rotate: g must be 16-byte aligned");
+  EXL3_REQUIRE(aligned(g, 16) && aligned(svh, 16) && aligned(y, out_dtype == EXL3_DTYPE_F32 ? 32 : 16), EXL3_ERR_ARG,
+               "exl3_prefill_out_rotate: g and svh must be 16-byte aligned, y 16-byte (32 for fp32)");
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int groups = rows * (n / 128);
   const int grid = (groups + 15) / 16;
