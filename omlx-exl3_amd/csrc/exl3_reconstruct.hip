@@ -2,11 +2,11 @@
 // Trellis -> fp16 weights, bit-exact (replaces decode_wt, reference src/omlx/exl3/kernels.py:304-351),
 // the codebook diagnostic, and the library's version / error entry points.
 //
-// Reconstruct: one thread per (output column pair, k-tile) run: it reads the run's K stream words plus the
-// word before, decodes 32 weights (columns g and 8+g of the tile, all 16 k) and writes two contiguous
-// 32-byte row segments of W_inner^T. Threads are ordered k-tile fastest, so a wavefront writes 64
-// consecutive segments of the same two output rows (2 KiB contiguous each): the kernel is bound by its
-// 2 bytes/weight of HBM writes (plus K/8 bytes/weight of reads).
+// Reconstruct: a workgroup takes a block of 4 k-tiles x 8 n-tiles; each thread decodes one run (32 weights:
+// columns g and 8+g of a tile, all 16 k), the 64 lanes of a wavefront reading 8 adjacent tiles' words
+// contiguously, into a padded LDS block of W_inner^T; then 8 consecutive lanes write each row's 128 bytes.
+// Both the trellis reads and the fp16 writes are whole cache lines: the kernel is bound by its 2 bytes per
+// weight of HBM writes (plus K/8 bytes per weight of reads).
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
@@ -25,37 +25,51 @@ void set_error(const char* fmt, ...) {
   va_end(ap);
 }
 
+constexpr int kRcNT = 8;      // n-tiles per workgroup: 128 rows of W_inner^T
+constexpr int kRcKT = 4;      // k-tiles per workgroup: 64 values of each row
+constexpr int kRcPitch = 33;  // LDS row pitch in words (odd: rows start on different banks)
+
 template <int K, int CB>
 __global__ __launch_bounds__(256) void reconstruct_kernel(const uint32_t* __restrict__ tr, int KT, int NT, int nt0,
                                                           int ntc, uint16_t* __restrict__ w) {
   constexpr int TW = 8 * K;
-  const size_t gid = (size_t)blockIdx.x * 256 + threadIdx.x;
-  const size_t total = (size_t)ntc * 8 * KT;
-  if (gid >= total) return;
-  const int kt = (int)(gid % (size_t)KT);
-  const int rg = (int)(gid / (size_t)KT);
-  const int g = rg & 7, ntl = rg >> 3;
-  const uint32_t* tp = tr + ((size_t)kt * NT + nt0 + ntl) * TW;
-  uint32_t wv[K];
+  __shared__ uint32_t sw[kRcNT * 16 * kRcPitch];
+  const int t = threadIdx.x;
+  const int ktl = t >> 6, ntl = (t >> 3) & 7, g = t & 7;   // the 64 lanes of a wavefront read 8 adjacent tiles
+  const int ktb = blockIdx.y * kRcKT, ntb = blockIdx.x * kRcNT;
+  const int kt = ktb + ktl, nt = ntb + ntl;
+  if (kt < KT && nt < ntc) {
+    const uint32_t* tp = tr + ((size_t)kt * NT + nt0 + nt) * TW;
+    uint32_t wv[K];
 #pragma unroll
-  for (int i = 0; i < K; ++i) wv[i] = tp[K * g + i];
-  const uint32_t wp = tp[(K * g + TW - 1) % TW];
-
-  uint32_t lo[8] = {}, hi[8] = {};
-  static_for<0, 32>([&](auto P) {
-    constexpr int p = decltype(P)::value;
-    using W = Win<K, p>;
-    const uint16_t v = dec_one<CB>(hash_pos<CB, K, p>(wv, wp));
-    uint32_t* dst = W::hi_col ? hi : lo;
-    dst[W::k_in >> 1] |= (uint32_t)v << (16 * (W::k_in & 1));
-  });
+    for (int i = 0; i < K; ++i) wv[i] = tp[K * g + i];
+    const uint32_t wp = tp[(K * g + TW - 1) % TW];
+    uint32_t lo[8] = {}, hi[8] = {};
+    static_for<0, 32>([&](auto P) {
+      constexpr int p = decltype(P)::value;
+      using W = Win<K, p>;
+      const uint16_t v = dec_one<CB>(hash_pos<CB, K, p>(wv, wp));
+      uint32_t* dst = W::hi_col ? hi : lo;
+      dst[W::k_in >> 1] |= (uint32_t)v << (16 * (W::k_in & 1));
+    });
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      sw[(ntl * 16 + g) * kRcPitch + ktl * 8 + j] = lo[j];
+      sw[(ntl * 16 + 8 + g) * kRcPitch + ktl * 8 + j] = hi[j];
+    }
+  }
+  __syncthreads();
+  // rows of W_inner^T: 8 consecutive lanes write one row's 128 bytes (64 k values)
   const size_t kk = (size_t)KT * 16;
-  u32x4* wlo = reinterpret_cast<u32x4*>(w + ((size_t)ntl * 16 + g) * kk + (size_t)kt * 16);
-  u32x4* whi = reinterpret_cast<u32x4*>(w + ((size_t)ntl * 16 + 8 + g) * kk + (size_t)kt * 16);
-  wlo[0] = u32x4{lo[0], lo[1], lo[2], lo[3]};
-  wlo[1] = u32x4{lo[4], lo[5], lo[6], lo[7]};
-  whi[0] = u32x4{hi[0], hi[1], hi[2], hi[3]};
-  whi[1] = u32x4{hi[4], hi[5], hi[6], hi[7]};
+  const int rows = min(kRcNT, ntc - ntb) * 16, kparts = 2 * min(kRcKT, KT - ktb);
+  for (int idx = t; idx < kRcNT * 16 * 8; idx += 256) {
+    const int r = idx >> 3, c = idx & 7;
+    if (r < rows && c < kparts) {
+      const uint32_t* src = sw + r * kRcPitch + 4 * c;
+      *reinterpret_cast<u32x4*>(w + (size_t)(ntb * 16 + r) * kk + (size_t)ktb * 16 + 8 * c) =
+          u32x4{src[0], src[1], src[2], src[3]};
+    }
+  }
 }
 
 // All 65,536 states through the GEMV's decode paths, with each state in either half of a register: 3INST /
@@ -85,9 +99,8 @@ __global__ __launch_bounds__(256) void codebook_kernel(uint16_t* __restrict__ ou
 
 template <int K, int CB>
 static void launch_reconstruct(const uint32_t* tr, int KT, int NT, int nt0, int ntc, uint16_t* w, hipStream_t st) {
-  const size_t total = (size_t)ntc * 8 * KT;
-  const unsigned blocks = (unsigned)((total + 255) / 256);
-  reconstruct_kernel<K, CB><<<blocks, 256, 0, st>>>(tr, KT, NT, nt0, ntc, w);
+  const dim3 grid((ntc + kRcNT - 1) / kRcNT, (KT + kRcKT - 1) / kRcKT);
+  reconstruct_kernel<K, CB><<<grid, 256, 0, st>>>(tr, KT, NT, nt0, ntc, w);
 }
 
 template <int CB>
