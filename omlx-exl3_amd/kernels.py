@@ -238,7 +238,7 @@ class TrellisGemvPlan:
 
 # Row count from which prefill_gemm's "auto" path takes the library-GEMM form (exl3_prefill_gemm_lib)
 # instead of the fused reconstruct-in-LDS kernel (exl3_prefill_gemm).
-PREFILL_LIBRARY_ROWS = 1024
+PREFILL_LIBRARY_ROWS = 64
 
 
 def prefill_gemm(xh: torch.Tensor, trellis: torch.Tensor, k: int, n: int, K: int, cb: int, svh: torch.Tensor,
