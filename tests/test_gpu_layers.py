@@ -215,3 +215,69 @@ def test_loader_end_to_end_on_gpu(pk, tmp_path):
         y = getattr(att, name)(x)
         ref = O.linear_ref(x.float().cpu().numpy(), tr, k, n, K, 0, suh, svh)
         assert O.max_abs_rel(y.float().cpu().numpy(), ref) < 2e-3, name
+
+
+def test_decoder_matches_fp32_reference_built_from_reconstructed_weights(pk):
+    """The synthetic decoder (prefill, then fused graph-ready decode steps) against an independent fp32
+    formulation of the same model: every EXL3 linear as had128(had128(x * suh) @ W_inner) * svh with W_inner
+    from decode_wt (bit-exact, oracle-pinned), RMSNorm, rotate-half rotary embedding, causal GQA attention,
+    SwiGLU, residuals, all in fp32 from the same parameters. The decoder keeps fp16 activations, so its
+    logits differ by fp16 rounding only: within 2% of the logit range, and its greedy token is the
+    reference's or within that margin of it."""
+    import math
+    from omlx_exl3_amd.synthetic import DecoderConfig, SyntheticDecoder, greedy_step
+
+    torch.manual_seed(0)
+    cfg = DecoderConfig(n_layers=2, hidden=256, intermediate=512, n_heads=4, n_kv_heads=2, head_dim=128,
+                        vocab=1024, max_len=64)
+    model = SyntheticDecoder(cfg, seed=4, device="cuda")
+
+    def had(v):
+        H = torch.tensor(O.sylvester(128), dtype=torch.float32, device=v.device) / math.sqrt(128)
+        r, n = v.shape
+        return (v.reshape(r, n // 128, 128) @ H).reshape(r, n)
+
+    def lin(l, x):
+        W = pk.kernels.decode_wt(l.trellis, l.in_features, l.out_features, l._K, l._cb).float()
+        return had(had(x * l._suh.float()) @ W.t()) * l._svh.float()
+
+    def rms(norm, x):
+        return x * torch.rsqrt((x * x).mean(-1, keepdim=True) + cfg.eps) * norm.weight.float()
+
+    def reference(ids):
+        T, nh, nkv, hd = ids.numel(), cfg.n_heads, cfg.n_kv_heads, cfg.head_dim
+        h = model.model.embed_tokens.weight[ids].float()
+        c, s = model.rope_cos[:T].unsqueeze(1), model.rope_sin[:T].unsqueeze(1)
+        causal = torch.ones(T, T, dtype=torch.bool, device="cuda").triu(1)
+        for layer in model.model.layers:
+            a = layer.self_attn
+            xn = rms(layer.input_layernorm, h)
+            q = lin(a.q_proj, xn).view(T, nh, hd)
+            k = lin(a.k_proj, xn).view(T, nkv, hd)
+            v = lin(a.v_proj, xn).view(T, nkv, hd)
+            rh = lambda x: torch.cat((-x[..., hd // 2:], x[..., :hd // 2]), dim=-1)  # noqa: E731
+            q, k = q * c + rh(q) * s, k * c + rh(k) * s
+            k, v = k.repeat_interleave(nh // nkv, dim=1), v.repeat_interleave(nh // nkv, dim=1)
+            sc = torch.matmul(q.permute(1, 0, 2).contiguous(), k.permute(1, 2, 0).contiguous()) / math.sqrt(hd)
+            p = torch.softmax(sc.masked_fill(causal, float("-inf")), dim=-1)                    # (nh, T, T)
+            o = torch.matmul(p, v.permute(1, 0, 2).contiguous()).permute(1, 0, 2).reshape(T, nh * hd)
+            h = h + lin(a.o_proj, o)
+            xn = rms(layer.post_attention_layernorm, h)
+            m = torch.nn.functional.silu(lin(layer.mlp.gate_proj, xn)) * lin(layer.mlp.up_proj, xn)
+            h = h + lin(layer.mlp.down_proj, m)
+        return lin(model.lm_head, rms(model.model.norm, h))[-1]
+
+    def close(got, want):
+        err = ((got - want).abs().max() / (want.max() - want.min())).item()
+        assert err < 2e-2, err
+        top = int(torch.argmax(got))
+        assert (want.max() - want[top]).item() <= 2e-2 * (want.max() - want.min()).item()
+
+    ids = torch.randint(0, cfg.vocab, (12,), device="cuda", generator=torch.Generator(device="cuda").manual_seed(5))
+    seq = ids.clone()
+    close(model(ids, torch.arange(12, device="cuda")), reference(seq))
+    tok, pos = torch.tensor([7], device="cuda"), torch.tensor([12], device="cuda")
+    for _ in range(4):
+        seq = torch.cat((seq, tok))
+        greedy_step(model, tok, pos)
+        close(model.last_logits, reference(seq))
