@@ -11,9 +11,11 @@ Inputs (rotated activations, trellis, svh) are resident in HBM before timing sta
 
   value          whole-job GB/s: algorithmic bytes of all timed steps / wall time of the timed region
                  (the steps replayed from one captured HIP graph, so host launch cost is excluded)
-  roofline       the GEMV kernel: algorithmic bytes per launch / its average launch duration, measured with
-                 HIP events on the launch stream, against the 8 TB/s HBM3E peak; traffic = HBM bytes per
-                 launch from rocprofv3 FETCH_SIZE / WRITE_SIZE (profiles/), or null
+  roofline       the GEMV kernel: algorithmic bytes per launch / its average launch duration = GPU time
+                 between HIP events recorded on the replay stream around the timed replays, divided by
+                 their launches; against the 8 TB/s HBM3E peak; traffic = HBM bytes per launch from
+                 rocprofv3 FETCH_SIZE / WRITE_SIZE (profiles/), or null. per_shape: medians of single
+                 eager launches bracketed by events (they include each launch's dispatch latency)
   cpu_baseline   the NumPy oracle (reconstruct + fp32 matmul + Hadamard + svh) on the q projection
   mixed_k        config 3: the 27B projections with K drawn per tensor from {2,3,4,5,6,8}, rows 1 / 2 / 4 / 8
   prefill        config 4: M = 4608 through gate / up / down at K = 6, TFLOP/s against the fp16 MFMA peak
@@ -409,13 +411,8 @@ def main() -> int:
             e.record()
             evs.append((name, nbytes, s, e))
     torch.cuda.synchronize()
-    tot_bytes = tot_ms = 0.0
     for name, nbytes, s, e in evs:
-        ms = s.elapsed_time(e)
-        per[name].append((nbytes, ms))
-        tot_bytes += nbytes
-        tot_ms += ms
-    kernel_gbs = tot_bytes / tot_ms / 1e6
+        per[name].append((nbytes, s.elapsed_time(e)))
     per_shape = {}
     for name, rec in per.items():
         nb = rec[0][0]
@@ -443,18 +440,25 @@ def main() -> int:
         if not torch.equal(it[4], r):
             print("graph replay differs from the eager result", file=sys.stderr)
             return 1
+    # HIP events on the replay stream bracket the timed replays: the GPU time of the timed region divided
+    # by its launches is the average launch duration (back-to-back launches, as rocprofv3 sees them)
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    ev0.record()
     for _ in range(reps):
         graph.replay()
+    ev1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     steps = reps * L
     value = step_bytes * steps / wall / 1e9
 
     traffic = read_traffic(args.traffic_file)
-    per_launch_bytes = tot_bytes / len(evs)
-    avg_launch_ms = tot_ms / len(evs)
+    n_launch = steps * len(layers[0])
+    per_launch_bytes = step_bytes / len(layers[0])
+    avg_launch_ms = ev0.elapsed_time(ev1) / n_launch
+    kernel_gbs = per_launch_bytes / avg_launch_ms / 1e6
     result = {
         "metric": METRIC,
         "value": round(value, 1),
