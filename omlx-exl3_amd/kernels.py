@@ -236,7 +236,7 @@ class TrellisGemvPlan:
         return self.fused(PROLOGUE_SWIGLU, gu, trellises, suh=suh, **kw)
 
 
-# Row count from which prefill_gemm's "auto" path takes the library-GEMM form (exl3_prefill_gemm_lib)
+# Row count from which prefill_gemm's "auto" path takes the library-GEMM form (reconstruct, BLAS, exl3_prefill_out_rotate)
 # instead of the fused reconstruct-in-LDS kernel (exl3_prefill_gemm).
 PREFILL_LIBRARY_ROWS = 64
 
