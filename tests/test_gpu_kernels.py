@@ -424,3 +424,27 @@ def test_gemv_table_kernel_wide_shape(pk, rows):
     assert O.max_abs_rel(ys[0].cpu().numpy(), ys[1].cpu().numpy()) < 1e-4
     again = pk.kernels.TrellisGemvPlan(k, ns, K, 0, svh, rows, torch.float32, table=True)(xh, trs)
     assert torch.equal(again, ys[0])
+
+
+@pytest.mark.parametrize("k,ns", [(16, [128]), (48, [128, 256]), (1040, [384]), (272, [128, 128, 128])])
+@pytest.mark.parametrize("K", [1, 8])
+def test_gemv_small_and_ragged_k(pk, k, ns, K):
+    """Shapes at the edges of the split choice: one k-tile, k-tile counts that are not a multiple of the
+    4-k-tile step, one-block outputs (a split of every k-tile, splits shorter than a k-group's share), at
+    rows 1 and the 16-row maximum, fp32 output against the oracle."""
+    for rows in (1, 16):
+        y, ref = _gemv_case(pk, k, ns, K, 0, rows, torch.float32, False, seed=k + K + rows)
+        assert O.max_abs_rel(y.cpu().numpy(), ref) < 2e-3, (k, ns, K, rows)
+
+
+@pytest.mark.parametrize("rows,path", [(9, "fused"), (9, "library"), (64, "auto"), (63, "auto")])
+def test_prefill_row_count_edges(pk, rows, path):
+    """The smallest prefill row count and the two sides of the library-form threshold, vs the oracle."""
+    k, n, K = 256, 256, 6
+    rng = np.random.default_rng(rows)
+    tr = O.random_trellis(k, n, K, 77)
+    svh = (rng.standard_normal(n) * 0.05).astype(np.float16)
+    xh = rng.standard_normal((rows, k)).astype(np.float16)
+    ref = O.gemv_ref(xh, O.reconstruct_inner(tr, k, n, K, 0), svh)
+    y = pk.kernels.prefill_gemm(dev(xh), dev(tr), k, n, K, 0, dev(svh), out_dtype=torch.float32, path=path)
+    assert O.max_abs_rel(y.cpu().numpy(), ref) < 2e-3
