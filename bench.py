@@ -90,7 +90,7 @@ def _cpu_reconstruct_cols(args):
 def cpu_baseline(seconds_budget: float = 30.0) -> dict:
     """NumPy oracle on the q projection (5120 -> 6144, K = 6): bit-exact reconstruct (column ranges in
     parallel worker processes, one per visible core), rotation, fp32 matmul, output Hadamard * svh. Median
-    of 3 runs after one warm-up."""
+    of 7 runs after one warm-up: about 1 s of wall time, 15-20 s of CPU work on 16 cores."""
     import concurrent.futures
     import multiprocessing
 
@@ -126,7 +126,7 @@ def cpu_baseline(seconds_budget: float = 30.0) -> dict:
     t_start = time.perf_counter()
     run()
     recs, mats = [], []
-    for _ in range(3):
+    for _ in range(7):
         a, b, _y = run()
         recs.append(a)
         mats.append(b)
