@@ -8,8 +8,8 @@
 //   k-groups of one wavefront; wavefront (cw, kg) owns n-tiles 2cw, 2cw+1 of the block and the split's
 //   iterations kg, kg + WK, ... Lane l = 16q + c decodes run g = c%8 of n-tile (2cw + c/8) for k-tile
 //   (kt0 + 4i + q) in iteration i: one wavefront iteration streams 8 tiles (4 k-tiles x 2 n-tiles).
-//   WK (1 or 2; the kernel takes any) depends only on the shape: narrow outputs have few workgroups, and
-//   more k-groups give each SIMD more wavefronts to interleave.
+//   WK (1 or 2, the most the kernel's launch bound allows) depends only on the shape: narrow outputs have
+//   few workgroups, and more k-groups give each SIMD more wavefronts to interleave.
 //
 // Contraction on MFMA (v_mfma_f32_16x16x32_f16): the decoded weights of a lane are the B operand as they
 // come out of the decoder (lane l = column c, k-group q), the activations are the A operand (row = batch
@@ -238,7 +238,8 @@ __device__ void prologue_finish(const GemvArgs& a, const ProPre& p, int kt0, int
 }
 
 template <int K, int CB, int L, int OT>
-__global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
+// 512 threads at most (WK <= 2); at most 96 VGPRs, so five wavefronts share each SIMD
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(5))) void gemv_kernel(GemvArgs a) {
   constexpr bool SPLIT = L == kSplit;
   constexpr int TW = 8 * K;
   constexpr int D = kDepth;
