@@ -251,7 +251,7 @@ def prefill_benchmark(pk, torch, dev, rows=4608, reps=3) -> dict:
     tf = {p: tot[p][0] / tot[p][1] / 1e9 for p in tot}
     return {"rows": rows, "path": auto, "per_proj": per[auto], "TFLOP_s": round(tf[auto], 1),
             "peak_TFLOP_s": MFMA_F16_PEAK_TFLOPS, "mfma_frac": round(tf[auto] / MFMA_F16_PEAK_TFLOPS, 4),
-            "ms_total": round(tot[auto][1], 2),
+            "ms_total": round(tot[auto][1], 2), "gemm_table": pk.kernels._gemm_table_loaded(),
             "by_path": {p: {"TFLOP_s": round(tf[p], 1), "ms_total": round(tot[p][1], 2), "per_proj": per[p]}
                         for p in per}}
 

@@ -11,6 +11,7 @@ kernels.py:269-270, 465); the C library re-validates and its status becomes an E
 from __future__ import annotations
 
 import ctypes
+import os
 
 import torch
 
@@ -236,6 +237,44 @@ class TrellisGemvPlan:
         return self.fused(PROLOGUE_SWIGLU, gu, trellises, suh=suh, **kw)
 
 
+# GEMM solution table of the library-GEMM prefill form: PyTorch TunableOp's CSV, made on MI355X by
+# tune_gemm.py for the 27B projection shapes at 64..4608 rows (the fastest hipBLASLt / rocBLAS solution of each
+# shape, which hipBLASLt's default heuristic does not always pick: 15-18% faster GEMMs at 4608 rows).
+GEMM_TABLE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "tuning", "prefill_gemm_mi355x.csv")
+_gemm_table_state: bool | None = None   # None: not read yet
+
+
+def _gemm_table_loaded() -> bool:
+    global _gemm_table_state
+    if _gemm_table_state is None:
+        ok = False
+        if os.path.exists(GEMM_TABLE):
+            try:
+                ok = bool(torch.cuda.tunable.read_file(GEMM_TABLE))   # False if its version lines do not match
+            except RuntimeError:
+                ok = False
+        _gemm_table_state = ok
+    return _gemm_table_state
+
+
+def library_gemm(a: torch.Tensor, wt: torch.Tensor, tuned: bool = True) -> torch.Tensor:
+    """a (rows, k) @ wt (n, k)^T in fp16 with fp32 accumulation, by the process's BLAS library (torch.matmul).
+    With tuned=True and GEMM_TABLE readable, TunableOp is switched on around this one call with tuning off, so
+    a shape in the table runs its recorded solution and any other shape the library default; the caller's
+    TunableOp settings are restored afterwards (nothing is tuned or written)."""
+    if not (tuned and _gemm_table_loaded()):
+        return torch.matmul(a, wt.t())
+    tun = torch.cuda.tunable
+    was_on, was_tuning = tun.is_enabled(), tun.tuning_is_enabled()
+    tun.tuning_enable(False)
+    tun.enable(True)
+    try:
+        return torch.matmul(a, wt.t())
+    finally:
+        tun.enable(was_on)
+        tun.tuning_enable(was_tuning)
+
+
 # Row count from which prefill_gemm's "auto" path takes the library-GEMM form (reconstruct, BLAS, exl3_prefill_out_rotate)
 # instead of the fused reconstruct-in-LDS kernel (exl3_prefill_gemm).
 PREFILL_LIBRARY_ROWS = 64
@@ -243,12 +282,13 @@ PREFILL_LIBRARY_ROWS = 64
 
 def prefill_gemm(xh: torch.Tensor, trellis: torch.Tensor, k: int, n: int, K: int, cb: int, svh: torch.Tensor,
                  bias: torch.Tensor | None = None, out_dtype: torch.dtype = torch.float16,
-                 out: torch.Tensor | None = None, path: str = "auto") -> torch.Tensor:
+                 out: torch.Tensor | None = None, path: str = "auto", tuned_gemm: bool = True) -> torch.Tensor:
     """had128(xh @ W_inner) * svh (+ bias) for xh (rows, k) fp16 (already rotated) (linear.py:97-105).
     path "fused": weights reconstructed in LDS and contracted on MFMA in one launch (exl3_prefill_gemm);
     "library": the reference's structure - W_inner^T reconstructed once (exl3_reconstruct), an fp16 GEMM with
     fp32 accumulation by the process's BLAS library (hipBLASLt through torch.matmul), then the output rotation
-    (exl3_prefill_out_rotate); "auto": the library form from PREFILL_LIBRARY_ROWS rows."""
+    (exl3_prefill_out_rotate); "auto": the library form from PREFILL_LIBRARY_ROWS rows. tuned_gemm: the
+    library form's GEMM runs the solution GEMM_TABLE records for its shape (library_gemm)."""
     _dev(xh, "xh")
     rows = xh.numel() // k
     _require(xh.dtype == torch.float16 and xh.numel() == rows * k, "xh must be fp16 (rows, k)")
@@ -261,7 +301,7 @@ def prefill_gemm(xh: torch.Tensor, trellis: torch.Tensor, k: int, n: int, K: int
         wt = torch.empty((n, k), dtype=torch.float16, device=xh.device)
         check(lib().exl3_reconstruct(ptr(trellis), k, n, K, cb, 0, n // 16, ptr(wt), stream_handle(xh.device)),
               "exl3_reconstruct")
-        g = torch.matmul(xh.reshape(rows, k), wt.t())
+        g = library_gemm(xh.reshape(rows, k), wt, tuned=tuned_gemm)
         check(lib().exl3_prefill_out_rotate(ptr(g), rows, n, ptr(svh), ptr(bias), ptr(out), DTYPE_CODE[out_dtype],
                                             stream_handle(xh.device)), "exl3_prefill_out_rotate")
         return out
@@ -301,4 +341,4 @@ def attn_decode_rotate(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, k_cach
 
 
 __all__ = ["MAX_GEMV_ROWS", "GEMV_ROWS_LIMIT", "TrellisGemvPlan", "decode_wt", "rot", "norm_rot", "swiglu_rot",
-           "prefill_gemm", "codebook", "attn_decode_rotate", "Exl3Error"]
+           "prefill_gemm", "library_gemm", "GEMM_TABLE", "codebook", "attn_decode_rotate", "Exl3Error"]

@@ -292,6 +292,29 @@ def test_prefill_library_path_matches_fused_with_bias(pk, dt):
     assert torch.equal(again, ys[1])
 
 
+def test_prefill_tuned_gemm_matches_default_and_restores_tunableop(pk):
+    """The library form with the GEMM solution table (a 27B down_proj shape the table lists at 512 rows) against
+    the library default: within the GEMM bar of each other and of the oracle-built product; TunableOp's
+    switches are back to the caller's values afterwards."""
+    F = pk.kernels
+    tun = torch.cuda.tunable
+    before = (tun.is_enabled(), tun.tuning_is_enabled())
+    k, n, K, rows = 17408, 5120, 6, 512
+    g = torch.Generator(device="cuda").manual_seed(22)
+    tr = torch.randint(-32768, 32768, (k // 16, n // 16, 16 * K), dtype=torch.int16, device="cuda", generator=g)
+    svh = (torch.randn(n, device="cuda", generator=g) * 0.01).half()
+    xh = torch.randn((rows, k), device="cuda", generator=g).half()
+    y_def = F.prefill_gemm(xh, tr, k, n, K, 0, svh, out_dtype=torch.float32, path="library", tuned_gemm=False)
+    y_tab = F.prefill_gemm(xh, tr, k, n, K, 0, svh, out_dtype=torch.float32, path="library", tuned_gemm=True)
+    assert (tun.is_enabled(), tun.tuning_is_enabled()) == before
+    assert ((y_tab - y_def).abs().max() / y_def.abs().max()).item() < 2e-3
+    W = F.decode_wt(tr, k, n, K, 0).float()
+    ref = _had128_t(xh.float() @ W.T) * svh.float()
+    assert ((y_tab - ref).abs().max() / ref.abs().max()).item() < 2e-3
+    if not F._gemm_table_loaded():
+        pytest.skip("GEMM solution table not accepted by this PyTorch / ROCm build (its version lines differ)")
+
+
 def test_prefill_out_rotate_vs_torch_and_rejects(pk):
     """The output rotation alone: fp16(H128(g)/sqrt(128) * svh) per 128-column block, bit-exact against the
     rotation written in torch (fp32 butterflies in the same stage order); bad shapes are refused."""

@@ -268,3 +268,22 @@ def test_synthetic_decoder_structure():
     assert full.layer_trellis_bytes() == 255_590_400 and full.head_trellis_bytes() == 583_434_240
     v = torch.tensor([0.5, 3.0, -1.0] * 100 + [7.0] + [0.0] * 50)
     assert synthetic.greedy_step.argmax(v).item() == 300
+
+
+def test_prefill_gemm_table_is_well_formed():
+    """The library prefill form's GEMM solution table (TunableOp CSV): version lines for this PyTorch build and
+    gfx950, and one entry per 27B projection shape at the row counts the benchmarks use (512, 4608), each
+    naming a hipBLASLt / rocBLAS solution or the library default. The GEMM is torch.matmul(x, wt.t()) with x
+    (rows, k) and wt (n, k), which PyTorch runs as the column-major "TN" product of M = n, N = rows, K = k."""
+    from omlx_exl3_amd import kernels
+    lines = [ln.strip().split(",") for ln in open(kernels.GEMM_TABLE) if ln.strip()]
+    val = {f[1]: f[2] for f in lines if f[0] == "Validator"}
+    assert val["PT_VERSION"] == torch.__version__.split("+")[0]
+    assert val["GCN_ARCH_NAME"].startswith("gfx950")
+    assert "HIPBLASLT_VERSION" in val and "ROCBLAS_VERSION" in val
+    entries = {f[1]: f[2] for f in lines if f[0] == "GemmTunableOp_Half_TN"}
+    assert len(entries) + len(val) == len(lines)
+    for rows in (512, 4608):
+        for k, n in [(5120, 6144), (5120, 1024), (6144, 5120), (5120, 17408), (17408, 5120)]:
+            sol = entries[f"tn_{n}_{rows}_{k}_ld_{k}_{k}_{n}"]
+            assert sol == "Default" or sol.split("_")[:2] in (["Gemm", "Hipblaslt"], ["Gemm", "Rocblas"])
