@@ -238,7 +238,7 @@ class TrellisGemvPlan:
 
 
 # GEMM solution table of the library-GEMM prefill form: PyTorch TunableOp's CSV, made on MI355X by
-# tune_gemm.py for the 27B projection shapes at 64..4608 rows (the fastest hipBLASLt / rocBLAS solution of each
+# tune_gemm.py for the 27B projection shapes at 16..4608 rows (the fastest hipBLASLt / rocBLAS solution of each
 # shape, which hipBLASLt's default heuristic does not always pick: 15-18% faster GEMMs at 4608 rows).
 GEMM_TABLE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "tuning", "prefill_gemm_mi355x.csv")
 _gemm_table_state: bool | None = None   # None: not read yet
@@ -276,8 +276,11 @@ def library_gemm(a: torch.Tensor, wt: torch.Tensor, tuned: bool = True) -> torch
 
 
 # Row count from which prefill_gemm's "auto" path takes the library-GEMM form (reconstruct, BLAS, exl3_prefill_out_rotate)
-# instead of the fused reconstruct-in-LDS kernel (exl3_prefill_gemm).
-PREFILL_LIBRARY_ROWS = 64
+# instead of the fused reconstruct-in-LDS kernel (exl3_prefill_gemm). With the GEMM solution table the library
+# form is the faster one from the smallest prefill (MAX_GEMV_ROWS + 1 rows) on: a 27B layer's seven projections
+# at 9 rows take 0.48 ms against 0.71 ms fused (measured on MI355X; only gate/up-sized outputs are ~10% faster
+# fused at 9-16 rows). The fused kernel stays selectable with path="fused".
+PREFILL_LIBRARY_ROWS = MAX_GEMV_ROWS + 1
 
 
 def prefill_gemm(xh: torch.Tensor, trellis: torch.Tensor, k: int, n: int, K: int, cb: int, svh: torch.Tensor,

@@ -24,7 +24,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 DEFAULT_OUT = os.path.join(HERE, "tuning", "prefill_gemm_mi355x.csv")
 # (k, n) of the 27B decoder's linear layers: q, k/v, o, gate/up, down
 SHAPES = [(5120, 6144), (5120, 1024), (6144, 5120), (5120, 17408), (17408, 5120)]
-ROWS = [64, 128, 256, 512, 1024, 2048, 4096, 4608]
+ROWS = [16, 32, 48, 64, 96, 128, 256, 512, 1024, 2048, 4096, 4608]
 
 
 def main() -> int:

@@ -460,9 +460,10 @@ def test_gemv_small_and_ragged_k(pk, k, ns, K):
         assert O.max_abs_rel(y.cpu().numpy(), ref) < 2e-3, (k, ns, K, rows)
 
 
-@pytest.mark.parametrize("rows,path", [(9, "fused"), (9, "library"), (64, "auto"), (63, "auto")])
+@pytest.mark.parametrize("rows,path", [(9, "fused"), (9, "library"), (9, "auto"), (63, "fused"), (64, "auto")])
 def test_prefill_row_count_edges(pk, rows, path):
-    """The smallest prefill row count and the two sides of the library-form threshold, vs the oracle."""
+    """The smallest prefill row count through both forms and the default, and a few more row counts,
+    vs the oracle."""
     k, n, K = 256, 256, 6
     rng = np.random.default_rng(rows)
     tr = O.random_trellis(k, n, K, 77)
