@@ -1,6 +1,6 @@
 #!/usr/bin/env python3
 # SPDX-License-Identifier: Apache-2.0
-"""Fused EXL3 decode GEMV throughput on one MI355X (BASELINE.json metric, config 2).
+"""Fused EXL3 decode GEMV throughput on one MI355X (the headline metric, on the 27B-class layer shapes).
 
 A step is one decode-layer pass of the EXL3 hot path at batch 1 on a 27B-class layer at K = 6 (6.0 bpw,
 3INST codebook), as the reference's fused decode path launches it (sibling groups, kernels.py:263-299,
@@ -339,7 +339,7 @@ def main() -> int:
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path (the EXL3 linear would shard "
-              "column-/row-parallel over RCCL, see DESIGN.md); run with --gpus 1", file=sys.stderr)
+              "column-parallel, row-parallel with an all-reduce over RCCL); run with --gpus 1", file=sys.stderr)
         return 2
 
     import torch

@@ -70,7 +70,7 @@ def test_reconstruct_random_all_codebooks(pk, K):
 
 
 def test_reconstruct_config1_bit_exact(pk):
-    """4096 x 4096 at K=4, uniform random bits, W bit-exact."""
+    """Config 1 (the reference's CPU-runnable case): 4096 x 4096 at K=4, uniform random bits, W bit-exact."""
     k = n = 4096
     tr_np = O.random_trellis(k, n, 4, 1)
     got = f16_bits(pk.kernels.decode_wt(dev(tr_np), k, n, 4, 0)).T
@@ -179,7 +179,7 @@ def test_gemv_all_bitrates_codebooks(pk, K, cb, fast):
 
 
 def test_gemv_config1(pk):
-    """BASELINE config 1 end to end: x -> rot -> GEMV vs the fp64 oracle linear."""
+    """Config 1 (4096 x 4096, K=4) end to end: x -> rot -> GEMV vs the fp64 oracle linear."""
     k = n = 4096
     rng = np.random.default_rng(11)
     tr = O.random_trellis(k, n, 4, 1)
