@@ -229,6 +229,27 @@ def test_gemv_27b_shapes_vs_reconstruct(pk, name):
         assert torch.equal(y1[0], y8[0])                              # row-exact
 
 
+@pytest.mark.parametrize("name,K,rows", [("qkv", 3, 4), ("o", 8, 2), ("gate_up", 2, 4), ("down", 5, 2),
+                                         ("gate_up", 4, 8), ("kv", 8, 1), ("q", 2, 2)])
+def test_gemv_27b_shapes_mixed_bitrates(pk, name, K, rows):
+    """Config 3's cases: full-size 27B projections at the other per-tensor bitrates {2, 3, 4, 5, 8} and batch
+    rows 1, 2, 4 and 8, against had128(xh @ W) * svh with W from the bit-exact reconstruct kernel and an fp32
+    matmul; row 0 equals the single-row result bit for bit."""
+    k, ns = SHAPES_27B[name]
+    g = torch.Generator(device="cuda").manual_seed(100 * K + rows)
+    trs = [torch.randint(-32768, 32768, (k // 16, n // 16, 16 * K), dtype=torch.int16, device="cuda", generator=g)
+           for n in ns]
+    svh = (torch.randn(sum(ns), device="cuda", generator=g) * 0.01).half()
+    xh = torch.randn((len(ns), rows, k), device="cuda", generator=g).half()
+    Ws = [pk.kernels.decode_wt(t, k, n, K, 0).float() for t, n in zip(trs, ns)]
+    ref = torch.cat([_had128_t(xh[m].float() @ Ws[m].T) for m in range(len(ns))], dim=1) * svh.float()
+    y = pk.kernels.TrellisGemvPlan(k, ns, K, 0, svh, rows, torch.float32)(xh, trs)
+    e = ((y - ref).abs().max() / ref.abs().max()).item()
+    assert e < 2e-3, (name, K, rows, e)
+    y1 = pk.kernels.TrellisGemvPlan(k, ns, K, 0, svh, 1, torch.float32)(xh[:, :1].contiguous(), trs)
+    assert torch.equal(y1[0], y[0])
+
+
 def test_gemv_bias_and_split_override(pk):
     k, n, K = 2048, 512, 6
     rng = np.random.default_rng(3)
