@@ -2,28 +2,32 @@
 # SPDX-License-Identifier: Apache-2.0
 """Fused EXL3 decode GEMV throughput on one MI355X (the headline metric, on the 27B-class layer shapes).
 
-A step is one decode-layer pass of the EXL3 hot path at batch 1 on a 27B-class layer at K = 6 (6.0 bpw,
-3INST codebook), as the reference's fused decode path launches it (sibling groups, kernels.py:263-299,
-linear.py:124-193): q/k/v (5120 -> 6144 + 1024 + 1024, one launch), o (6144 -> 5120), gate/up
-(5120 -> 17408 + 17408, one launch), down (17408 -> 5120). Steps rotate over `--layers` distinct layers
-(default 6 = 1.53 GB of trellis) so the weights stream from HBM, not from the 256 MB Infinity Cache.
-Inputs (rotated activations, trellis, svh) are resident in HBM before timing starts.
+A step is one decode token's pass of the EXL3 GEMV hot path at batch 1 through the layers of a 27B-class
+model at K = 6 (6.0 bpw, 3INST codebook): per layer the four launches the reference's fused decode path makes
+(sibling groups, kernels.py:263-299, linear.py:124-193): q/k/v (5120 -> 6144 + 1024 + 1024, one launch),
+o (6144 -> 5120), gate/up (5120 -> 17408 + 17408, one launch), down (17408 -> 5120), over `--layers`
+distinct layers (default 64, the model's depth: 16.4 GB of trellis), so the weights stream from HBM, not
+from the 256 MB Infinity Cache. One step is one replay of a HIP graph holding all of them; exactly --steps
+steps are timed (20 steps ~ 0.1 s). Inputs (rotated activations, trellis, svh) are resident in HBM before
+timing starts.
 
   value          whole-job GB/s: algorithmic bytes of all timed steps / wall time of the timed region
-                 (the steps replayed from one captured HIP graph, so host launch cost is excluded)
+                 (graph replays, so host launch cost is excluded)
   roofline       the GEMV kernel: algorithmic bytes per launch / its average launch duration = GPU time
                  between HIP events recorded on the replay stream around the timed replays, divided by
                  their launches; against the 8 TB/s HBM3E peak; traffic = HBM bytes per launch from
                  rocprofv3 FETCH_SIZE / WRITE_SIZE (profiles/), or null. per_shape: medians of single
                  eager launches bracketed by events (they include each launch's dispatch latency)
   cpu_baseline   the NumPy oracle (reconstruct + fp32 matmul + Hadamard + svh) on the q projection
-  mixed_k        config 3: the 27B projections with K drawn per tensor from {2,3,4,5,6,8}, rows 1 / 2 / 4 / 8
+  mixed_k        config 3: the 27B projections with K drawn per tensor from {2,3,4,5,6,8}, rows 1 / 2 / 4 / 8,
+                 whole layers back to back, and per K the GB/s of that K's launches (medians of single
+                 launches, so each includes its dispatch latency)
   prefill        config 4: M = 4608 through gate / up / down at K = 6, TFLOP/s against the fp16 MFMA peak
   decode_tok_s   end-to-end batch-1 greedy decode of the synthetic 27B-shape EXL3 decoder (config 5: 64
                  layers, hidden 5120, MLP 17408, GQA 48/8 x 128, head 5120 -> 151936, K = 6): a 512-token
                  random-id prompt, then 256 tokens, each decode step replayed from one captured HIP graph
 
-    python bench.py [--gpus 1] [--steps 240] [--warmup 24] [--mode exact|fast] [--decoder-layers 64]
+    python bench.py [--gpus 1] [--steps 60] [--warmup 5] [--mode exact|fast] [--decoder-layers 64]
 """
 from __future__ import annotations
 
@@ -212,9 +216,31 @@ def mixed_k_benchmark(pk, torch, dev, rows_list=(1, 2, 4, 8), n_layers=8, reps=4
         e.record()
         torch.cuda.synchronize()
         ms = s.elapsed_time(e) / reps
-        out["per_rows"][str(rows)] = {"us_per_layer": round(ms * 1e3 / n_layers, 1),
-                                      "GB_s": round(nbytes / ms / 1e6, 1),
-                                      "pct_hbm_peak": round(100 * nbytes / ms / 1e6 / HBM_PEAK_GBS, 1)}
+        # per K: single launches bracketed by events, median over the repetitions
+        evs = []
+        for _ in range(reps):
+            for i, (plan, xh, trs, o) in enumerate(items):
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record()
+                plan(xh, trs, out=o)
+                b.record()
+                evs.append((i, a, b))
+        torch.cuda.synchronize()
+        times = {}
+        for i, a, b in evs:
+            times.setdefault(i, []).append(a.elapsed_time(b))
+        per_k = {}
+        for i, (plan, _xh, _trs, _o) in enumerate(items):
+            d = per_k.setdefault(plan.K, [0, 0.0, 0])
+            d[0] += algorithmic_bytes(plan.k, plan.ns, plan.K, rows)
+            d[1] += statistics.median(times[i])
+            d[2] += 1
+        out["per_rows"][str(rows)] = {
+            "us_per_layer": round(ms * 1e3 / n_layers, 1), "GB_s": round(nbytes / ms / 1e6, 1),
+            "pct_hbm_peak": round(100 * nbytes / ms / 1e6 / HBM_PEAK_GBS, 1),
+            "per_K": {str(K): {"launches": d[2], "GB_s": round(d[0] / d[1] / 1e6, 1),
+                               "pct_hbm_peak": round(100 * d[0] / d[1] / 1e6 / HBM_PEAK_GBS, 1)}
+                      for K, d in sorted(per_k.items())}}
     return out
 
 
@@ -319,12 +345,12 @@ def decode_benchmark(pk, torch, dev, n_layers: int, prompt: int, gen: int) -> di
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=240)
-    ap.add_argument("--warmup", type=int, default=24)
+    ap.add_argument("--steps", type=int, default=60, help="timed steps (one step = one decode token's GEMVs)")
+    ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--mode", choices=["exact", "fast"], default="exact")
     ap.add_argument("--table", action="store_true",
                     help="the table GEMV kernel (LDS codebook lookup for half of each run) instead of hashing")
-    ap.add_argument("--layers", type=int, default=6, help="distinct layers in the rotating working set")
+    ap.add_argument("--layers", type=int, default=64, help="distinct 27B-shape layers per step")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--traffic-file", default=os.path.join(ROOT, "profiles", "gemv_27b_k6_traffic.txt"))
     ap.add_argument("--copy-probe", action="store_true",
@@ -394,16 +420,15 @@ def main() -> int:
         for _name, plan, xh, trs, out, _b in items:
             plan(xh, trs, out=out)
 
-    # warm-up (eager)
-    for i in range(args.warmup):
-        run_layer(layers[i % L])
+    # eager pass (plans, kernels)
+    for items in layers:
+        run_layer(items)
     torch.cuda.synchronize()
 
-    # ---- per-launch kernel durations (HIP events on the launch stream) ----
-    n_evt = max(L, (args.steps // L) * L)
+    # ---- per-launch kernel durations (HIP events on the launch stream), two eager passes ----
     per = {name: [] for name, _, _ in LAYER}
     evs = []
-    for i in range(n_evt):
+    for i in range(2 * L):
         for name, plan, xh, trs, out, nbytes in layers[i % L]:
             s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             s.record()
@@ -420,8 +445,7 @@ def main() -> int:
         per_shape[name] = {"bytes": nb, "median_us": round(med * 1e3, 2), "GB_s": round(nb / med / 1e6, 1),
                            "pct_hbm_peak": round(100 * nb / med / 1e6 / HBM_PEAK_GBS, 1)}
 
-    # ---- whole-job throughput: all layers captured in one graph, replayed ----
-    reps = max(1, args.steps // L)
+    # ---- whole-job throughput: one step = all layers' launches captured in one graph, replayed ----
     graph = torch.cuda.CUDAGraph()
     cap = torch.cuda.Stream(device=dev)
     cap.wait_stream(torch.cuda.current_stream(dev))
@@ -440,22 +464,24 @@ def main() -> int:
         if not torch.equal(it[4], r):
             print("graph replay differs from the eager result", file=sys.stderr)
             return 1
+    for _ in range(args.warmup):
+        graph.replay()
     # HIP events on the replay stream bracket the timed replays: the GPU time of the timed region divided
     # by its launches is the average launch duration (back-to-back launches, as rocprofv3 sees them)
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     ev0.record()
-    for _ in range(reps):
+    for _ in range(args.steps):
         graph.replay()
     ev1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    steps = reps * L
-    value = step_bytes * steps / wall / 1e9
+    steps = args.steps
+    value = step_bytes * L * steps / wall / 1e9
 
     traffic = read_traffic(args.traffic_file)
-    n_launch = steps * len(layers[0])
+    n_launch = steps * L * len(layers[0])
     per_launch_bytes = step_bytes / len(layers[0])
     avg_launch_ms = ev0.elapsed_time(ev1) / n_launch
     kernel_gbs = per_launch_bytes / avg_launch_ms / 1e6
@@ -467,14 +493,16 @@ def main() -> int:
         "steps": steps,
         "warmup": args.warmup,
         "ms_per_step": round(wall / steps * 1e3, 4),
+        "timed_s": round(wall, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp16",
         "data": "synthetic",
-        "config": {"workload": ("27B-class decode layer, batch 1, K=6 (6.0 bpw) 3INST: fused GEMV launches qkv "
-                                "5120->6144+1024+1024, o 6144->5120, gate_up 5120->17408+17408, down 17408->5120; "
-                                f"{L} distinct layers rotated ({step_bytes * L / 1e9:.2f} GB of weights)"),
+        "config": {"workload": ("27B-class decode GEMVs, batch 1, K=6 (6.0 bpw) 3INST; a step = one token through "
+                                f"{L} distinct layers of fused GEMV launches qkv 5120->6144+1024+1024, o 6144->5120, "
+                                "gate_up 5120->17408+17408, down 17408->5120 "
+                                f"({step_bytes * L / 1e9:.2f} GB of weights per step)"),
                    "global_batch": rows, "bpw": K, "codebook": "3inst", "gemv_mode": args.mode,
                    "gemv_kernel": "table" if (args.table and not fast) else "hash",
                    "parallelism": "none (1 GPU)"},

@@ -109,15 +109,20 @@ int exl3_gemv_ex(const uint16_t* xh, const uint32_t* const* trellis, int n_membe
  * (fp16) and exl3_gemv, bit for bit. Always the hashing kernel.
  * Prologue (how the rotated input is formed):
  *   EXL3_PROLOGUE_NONE     x is the rotated input xh (n_members, rows, k), as exl3_gemv's; residual,
- *                          residual_out, w, x_sumsq and suh NULL
+ *                          residual_out, xn_out, w, x_sumsq and suh NULL
  *   EXL3_PROLOGUE_RMSNORM  x fp16 (rows, k); residual NULL or fp16 (rows, k); h = fp16(x + residual) is
- *                          written to residual_out (NULL: not written; must not overlap x or residual);
- *                          w fp16 (k), eps: xh_m = rot(fp16(w * fp16(h * rsqrt(mean(h^2) + eps))), suh_m).
+ *                          written to residual_out (NULL: not written); w fp16 (k), eps:
+ *                          xn = fp16(w * fp16(h * rsqrt(mean(h^2) + eps))), written to xn_out (rows, k) when
+ *                          not NULL, and xh_m = rot(xn, suh_m). residual_out and xn_out must not overlap x,
+ *                          residual, w or each other.
  *                          x_sumsq: NULL, or with no residual the sums of squares of x's 128-blocks
  *                          (rows, k/128) fp64 as a previous call's y_sumsq wrote them, so the launch reads
  *                          only its own part of x
  *   EXL3_PROLOGUE_SWIGLU   x = gu fp16 (rows, 2k) = [gate | up], one member: xh = rot(silu(gate) * up, suh);
- *                          residual, residual_out, w and x_sumsq NULL
+ *                          residual, residual_out, xn_out, w and x_sumsq NULL
+ *   EXL3_PROLOGUE_ROTATE   x fp16 (rows, k): xh_m = rot(x, suh_m), the values exl3_rotate writes (the input
+ *                          rotation of an EXL3Linear call inside its GEMV launch); residual, residual_out,
+ *                          xn_out, w and x_sumsq NULL
  *   suh fp16 (n_members, k); k % 128 == 0 with a prologue.
  * Epilogue (fp16 output only): y = fp16(y + y_residual) when y_residual (rows, n_total) is given (the next
  * norm's residual add; y_residual may be y's own buffer), and y_sumsq (rows, n_total/128) fp64 receives each
@@ -125,8 +130,9 @@ int exl3_gemv_ex(const uint16_t* xh, const uint32_t* const* trellis, int n_membe
 #define EXL3_PROLOGUE_NONE 0
 #define EXL3_PROLOGUE_RMSNORM 1
 #define EXL3_PROLOGUE_SWIGLU 2
+#define EXL3_PROLOGUE_ROTATE 3
 int exl3_gemv_fused(int prologue, const uint16_t* x, const uint16_t* residual, uint16_t* residual_out,
-                    const uint16_t* w, float eps, const double* x_sumsq, const uint16_t* suh,
+                    uint16_t* xn_out, const uint16_t* w, float eps, const double* x_sumsq, const uint16_t* suh,
                     const uint32_t* const* trellis, int n_members, const int* member_n, int k, int K, int cb,
                     const uint16_t* svh, const void* bias, void* y, int out_dtype, int rows, unsigned flags,
                     const uint16_t* y_residual, double* y_sumsq, void* workspace, size_t workspace_bytes,
@@ -134,7 +140,7 @@ int exl3_gemv_fused(int prologue, const uint16_t* x, const uint16_t* residual, u
 
 /* Input rotation: xh[m, r, :] = fp16(H128(x[r, :] * suh[m, :]) / sqrt(128)) per 128-block, fp32 inside.
  * Replaces rot (kernels.py:388-406, 451-458). x (rows, k) in x_dtype; suh fp16 (n_members, k);
- * xh fp16 (n_members, rows, k). k % 128 == 0. */
+ * xh fp16 (n_members, rows, k). k % 128 == 0. xh must not overlap x or suh. */
 int exl3_rotate(const void* x, int x_dtype, const uint16_t* suh, int n_members, int rows, int k, uint16_t* xh,
                 void* stream);
 
@@ -144,14 +150,16 @@ int exl3_rotate(const void* x, int x_dtype, const uint16_t* suh, int n_members, 
  *   xn = T(w * T(h * rsqrt(mean(h^2) + eps)))                       (MLX's rounding of rms_norm)
  *   xh[m] = fp16(H128(xn * suh[m]) / sqrt(128))                     (skipped when n_members == 0)
  * x, residual, residual_out, w, xn: (rows, k) / (k) in dtype T = EXL3_DTYPE_F16 or BF16;
- * suh fp16 (n_members, k); xh fp16 (n_members, rows, k). k % 128 == 0. */
+ * suh fp16 (n_members, k); xh fp16 (n_members, rows, k). k % 128 == 0.
+ * Not in place: residual_out, xn and xh must not overlap x, residual, w or each other (a row is spread
+ * over several workgroups that each read the whole row while the others write); EXL3_ERR_ARG otherwise. */
 int exl3_rmsnorm_rotate(const void* x, const void* residual, void* residual_out, const void* w, int dtype,
                         float eps, const uint16_t* suh, int n_members, int rows, int k, void* xn, uint16_t* xh,
                         void* stream);
 
 /* Fused SwiGLU + rotation: xh[r, :] = fp16(H128(silu(gate) * up * suh) / sqrt(128)), gu = [gate | up].
  * Replaces swiglu_rot (kernels.py:427-433, 476-483). gu fp16 (rows, 2n); suh fp16 (n); xh fp16 (rows, n).
- * n % 128 == 0. */
+ * n % 128 == 0. xh must not overlap gu or suh. */
 int exl3_swiglu_rotate(const uint16_t* gu, const uint16_t* suh, int rows, int n, uint16_t* xh, void* stream);
 
 /* Prefill contraction: y = had128(xh @ W_inner) * svh (+ bias) for many rows, with trellis tiles

@@ -34,6 +34,13 @@ void set_error(const char* fmt, ...);
 
 inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
+// True when the byte ranges [a, a + an) and [b, b + bn) share a byte (a NULL pointer overlaps nothing).
+inline bool overlaps(const void* a, size_t an, const void* b, size_t bn) {
+  if (!a || !b || an == 0 || bn == 0) return false;
+  const uintptr_t a0 = reinterpret_cast<uintptr_t>(a), b0 = reinterpret_cast<uintptr_t>(b);
+  return a0 < b0 + bn && b0 < a0 + an;
+}
+
 // Device address of codebook cb's 65,536-entry fp16 lookup table on the current device (nullptr on failure).
 const uint16_t* codebook_table(int cb);
 

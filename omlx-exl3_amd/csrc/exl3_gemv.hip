@@ -35,10 +35,10 @@ namespace exl3 {
 // Prologue staging: the split's activations computed in the workgroup from the layer's un-rotated input
 // instead of read from xh. kProNorm: h = fp16(x + residual) and xn = fp16(w * fp16(h * inv_rms)) with the row's
 // sum of squares in fp64 (exact, so independent of the reduction order), as exl3_rmsnorm_rotate computes them;
-// kProSwiglu: silu(gate) * up as exl3_swiglu_rotate computes it. Then e = v * suh_m, the 128-point FWHT of
-// each block, * 1/sqrt(128), fp16: the values those kernels write to xh, so the GEMV's result is bit-identical
-// to rotating first. The workgroup of member 0's first block in each split also writes h for the split's
-// k-range. k is a multiple of 128 (checked on the host).
+// kProSwiglu: silu(gate) * up as exl3_swiglu_rotate computes it; kProRot: x itself. Then e = v * suh_m, the
+// 128-point FWHT of each block, * 1/sqrt(128), fp16: the values those kernels (and exl3_rotate) write to xh, so
+// the GEMV's result is bit-identical to rotating first. The workgroup of member 0's first block in each split
+// also writes h and xn for the split's k-range. k is a multiple of 128 (checked on the host).
 template <bool SPLIT>
 __device__ void stage_prologue(const GemvArgs& a, int m, int blk_in_member, int kt0, int kt1, int nrec, u32x4* xs,
                                double (*ss_part)[16], float* inv_rms) {
@@ -88,7 +88,9 @@ __device__ void stage_prologue(const GemvArgs& a, int m, int blk_in_member, int 
   }
   const int b0 = kt0 >> 3, b1 = (kt1 + 7) >> 3;   // 128-element blocks overlapping the split
   const int nb = (b1 - b0) * rows;
+  // member 0's first block writes h and xn for the split's k-range (each element once over the splits)
   const bool write_h = a.pro == kProNorm && a.pres_out != nullptr && m == 0 && blk_in_member == 0;
+  const bool write_xn = a.pro == kProNorm && a.pxn_out != nullptr && m == 0 && blk_in_member == 0;
   const uint16_t* __restrict__ suh = a.psuh + (size_t)m * k;
   // one 128-block of one row per 16-lane group (8 consecutive elements per lane); a group is active or idle
   // as a whole, and its FWHT exchanges stay inside the group
@@ -112,6 +114,9 @@ __device__ void stage_prologue(const GemvArgs& a, int m, int blk_in_member, int 
       const float inv = inv_rms[r];
 #pragma unroll
       for (int i = 0; i < 8; ++i) v[i] = round_through<kF16>(wv[i] * round_through<kF16>(v[i] * inv));
+      if (write_xn && in_split) store8<kF16>(a.pxn_out, (size_t)r * k + c0, v);
+    } else if (a.pro == kProRot) {
+      load8<kF16>(a.px, (size_t)r * k + c0, v);
     } else {
       float uv[8];
       load8<kF16>(a.px, (size_t)r * 2 * k + c0, v);
@@ -152,8 +157,8 @@ struct ProPre {
   bool valid;
 };
 
-// Early form of stage_prologue for one row with the sums of squares given (RMSNORM) or SwiGLU, when every
-// 128-block of the split has its own 16-lane group: issue the loads.
+// Early form of stage_prologue for one row with the sums of squares given (RMSNORM), SwiGLU or the rotation
+// alone, when every 128-block of the split has its own 16-lane group: issue the loads.
 __device__ __forceinline__ ProPre prologue_preload(const GemvArgs& a, int m, int kt0, int kt1) {
   ProPre p{};
   const int tid = threadIdx.x, lane = tid & 63, k = a.k;
@@ -162,7 +167,7 @@ __device__ __forceinline__ ProPre prologue_preload(const GemvArgs& a, int m, int
   if (p.valid) {
     const int c0 = (b0 + (tid >> 4)) * 128 + (lane & 15) * 8;
     p.x = *reinterpret_cast<const u32x4*>(a.px + c0);
-    p.w = *reinterpret_cast<const u32x4*>(a.pro == kProNorm ? a.pw + c0 : a.px + k + c0);
+    if (a.pro != kProRot) p.w = *reinterpret_cast<const u32x4*>(a.pro == kProNorm ? a.pw + c0 : a.px + k + c0);
     p.s = *reinterpret_cast<const u32x4*>(a.psuh + (size_t)m * k + c0);
   }
   if (a.pro == kProNorm && tid < k / 128) p.ss = a.pss[tid];
@@ -181,7 +186,7 @@ __device__ __forceinline__ void unpack8(const u32x4& q, float (&v)[8]) {
 // The rest of the early prologue, after the trellis prefetch: the same values as stage_prologue.
 template <bool SPLIT>
 __device__ void prologue_finish(const GemvArgs& a, const ProPre& p, int kt0, int kt1, int nrec, u32x4* xs,
-                                double (*ss_part)[16], float* inv_rms) {
+                                double (*ss_part)[16], float* inv_rms, bool write_xn) {
   constexpr int RW = SPLIT ? 4 : 2;
   const int tid = threadIdx.x, nthr = blockDim.x, lane = tid & 63, wave = tid >> 6, nw = nthr >> 6;
   const int nkt = kt1 - kt0;
@@ -212,7 +217,8 @@ __device__ void prologue_finish(const GemvArgs& a, const ProPre& p, int kt0, int
     const float inv = inv_rms[0];
 #pragma unroll
     for (int i = 0; i < 8; ++i) v[i] = round_through<kF16>(w[i] * round_through<kF16>(v[i] * inv));
-  } else {
+    if (write_xn && kt >= kt0 && kt < kt1) store8<kF16>(a.pxn_out, c0, v);
+  } else if (a.pro == kProSwiglu) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const float ex = (float)exp(-(double)v[i]);   // exp(-g) rounded once to fp32
@@ -318,7 +324,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(5))) void g
     else xs[idx] = v;
   };
   const int b_split = ((kt1 + 7) >> 3) - (kt0 >> 3);
-  const bool early_pro = a.pro != kProNone && rows == 1 && (a.pro == kProSwiglu || a.pss != nullptr) &&
+  const bool early_pro = a.pro != kProNone && rows == 1 && (a.pro != kProNorm || a.pss != nullptr) &&
                          b_split <= (nthr >> 4) && a.k / 128 <= nthr;
   ProPre pp{};
   u32x4 pre0 = {0u, 0u, 0u, 0u}, pre1 = {0u, 0u, 0u, 0u};
@@ -337,7 +343,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(5))) void g
 
   // ---- stage them in LDS, zero past the split ----
   if (early_pro) {
-    prologue_finish<SPLIT>(a, pp, kt0, kt1, nrec, xs, ss_part, inv_rms);
+    prologue_finish<SPLIT>(a, pp, kt0, kt1, nrec, xs, ss_part, inv_rms,
+                           a.pxn_out != nullptr && m == 0 && blk == blk0);
   } else if (a.pro != kProNone) {
     stage_prologue<SPLIT>(a, m, blk - blk0, kt0, kt1, nrec, xs, ss_part, inv_rms);
   } else {
@@ -611,6 +618,7 @@ struct GemvPrologueArgs {
   int mode;
   const uint16_t *x, *residual;
   uint16_t* residual_out;
+  uint16_t* xn_out;
   const uint16_t *w, *suh;
   float eps;
   const double* x_sumsq;
@@ -722,6 +730,7 @@ static int gemv_run(const uint16_t* xh, const GemvPrologueArgs& pro, const uint3
   a.px = pro.x;
   a.pres = pro.residual;
   a.pres_out = pro.residual_out;
+  a.pxn_out = pro.xn_out;
   a.pw = pro.w;
   a.eps = pro.eps;
   a.psuh = pro.suh;
@@ -747,27 +756,29 @@ extern "C" int exl3_gemv_ex(const uint16_t* xh, const uint32_t* const* trellis, 
                             int k, int K, int cb, const uint16_t* svh, const void* bias, void* y, int out_dtype,
                             int rows, unsigned flags, void* workspace, size_t workspace_bytes, int kt_per_split,
                             void* stream) {
-  const GemvPrologueArgs none{kProNone, nullptr, nullptr, nullptr, nullptr, nullptr, 0.f, nullptr, nullptr, nullptr};
+  const GemvPrologueArgs none{kProNone, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 0.f, nullptr, nullptr,
+                              nullptr};
   return gemv_run(xh, none, trellis, n_members, member_n, k, K, cb, svh, bias, y, out_dtype, rows, flags, workspace,
                   workspace_bytes, kt_per_split, stream);
 }
 
 extern "C" int exl3_gemv_fused(int prologue, const uint16_t* x, const uint16_t* residual, uint16_t* residual_out,
-                               const uint16_t* w, float eps, const double* x_sumsq, const uint16_t* suh,
+                               uint16_t* xn_out, const uint16_t* w, float eps, const double* x_sumsq, const uint16_t* suh,
                                const uint32_t* const* trellis, int n_members, const int* member_n, int k, int K,
                                int cb, const uint16_t* svh, const void* bias, void* y, int out_dtype, int rows,
                                unsigned flags, const uint16_t* y_residual, double* y_sumsq, void* workspace,
                                size_t workspace_bytes, void* stream) {
-  EXL3_REQUIRE(prologue == EXL3_PROLOGUE_NONE || prologue == EXL3_PROLOGUE_RMSNORM || prologue == EXL3_PROLOGUE_SWIGLU,
+  EXL3_REQUIRE(prologue == EXL3_PROLOGUE_NONE || prologue == EXL3_PROLOGUE_RMSNORM || prologue == EXL3_PROLOGUE_SWIGLU ||
+                   prologue == EXL3_PROLOGUE_ROTATE,
                EXL3_ERR_ARG, "exl3_gemv_fused: unknown prologue %d", prologue);
   EXL3_REQUIRE((y_residual == nullptr && y_sumsq == nullptr) || out_dtype == kF16, EXL3_ERR_ARG,
                "exl3_gemv_fused: y_residual and y_sumsq need an fp16 output");
   EXL3_REQUIRE(!y_sumsq || aligned(y_sumsq, 8), EXL3_ERR_ARG, "exl3_gemv_fused: y_sumsq must be 8-byte aligned");
   if (prologue == EXL3_PROLOGUE_NONE) {
-    EXL3_REQUIRE(!residual && !residual_out && !w && !x_sumsq && !suh, EXL3_ERR_ARG,
+    EXL3_REQUIRE(!residual && !residual_out && !xn_out && !w && !x_sumsq && !suh, EXL3_ERR_ARG,
                  "exl3_gemv_fused: without a prologue x is the rotated input and the prologue arguments are NULL");
-    const GemvPrologueArgs pro{kProNone, nullptr, nullptr, nullptr, nullptr, nullptr, 0.f, nullptr, y_residual,
-                               y_sumsq};
+    const GemvPrologueArgs pro{kProNone, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 0.f, nullptr,
+                               y_residual, y_sumsq};
     return gemv_run(x, pro, trellis, n_members, member_n, k, K, cb, svh, bias, y, out_dtype, rows, flags, workspace,
                     workspace_bytes, 0, stream);
   }
@@ -777,27 +788,34 @@ extern "C" int exl3_gemv_fused(int prologue, const uint16_t* x, const uint16_t* 
   EXL3_REQUIRE(aligned(x, 16) && aligned(suh, 16) && (!residual || aligned(residual, 16)) &&
                    (!residual_out || aligned(residual_out, 16)) && (!w || aligned(w, 16)),
                EXL3_ERR_ARG, "exl3_gemv_fused: x, residual, residual_out, w and suh must be 16-byte aligned");
+  EXL3_REQUIRE(!xn_out || (prologue == EXL3_PROLOGUE_RMSNORM && aligned(xn_out, 16)), EXL3_ERR_ARG,
+               "exl3_gemv_fused: xn_out (16-byte aligned) belongs to the RMSNORM prologue");
   if (prologue == EXL3_PROLOGUE_RMSNORM) {
     EXL3_REQUIRE(w != nullptr, EXL3_ERR_ARG, "exl3_gemv_fused: RMSNORM needs the norm weight");
     EXL3_REQUIRE(residual_out == nullptr || residual != nullptr, EXL3_ERR_ARG,
                  "exl3_gemv_fused: residual_out needs a residual");
     EXL3_REQUIRE(x_sumsq == nullptr || (residual == nullptr && aligned(x_sumsq, 8)), EXL3_ERR_ARG,
                  "exl3_gemv_fused: x_sumsq (8-byte aligned) describes x alone, so it takes no residual");
-    if (residual_out) {   // other workgroups read x and residual while h is written
-      const size_t bytes = (size_t)rows * k * 2;
-      auto overlaps = [&](const void* p) {
-        const char *a0 = static_cast<const char*>(p), *b0 = reinterpret_cast<const char*>(residual_out);
-        return a0 < b0 + bytes && b0 < a0 + bytes;
-      };
-      EXL3_REQUIRE(!overlaps(x) && !overlaps(residual), EXL3_ERR_ARG,
-                   "exl3_gemv_fused: residual_out must not overlap x or residual");
+    {   // other workgroups read x, residual and w while h and xn are written
+      const size_t rb = (size_t)rows * k * 2;
+      bool bad = false;
+      for (const void* o : {static_cast<const void*>(residual_out), static_cast<const void*>(xn_out)})
+        bad = bad || overlaps(o, rb, x, rb) || overlaps(o, rb, residual, rb) || overlaps(o, rb, w, (size_t)k * 2);
+      bad = bad || overlaps(residual_out, rb, xn_out, rb);
+      EXL3_REQUIRE(!bad, EXL3_ERR_ARG,
+                   "exl3_gemv_fused: residual_out and xn_out must not overlap x, residual, w or each other");
     }
-  } else {
+  } else if (prologue == EXL3_PROLOGUE_SWIGLU) {
     EXL3_REQUIRE(n_members == 1 && residual == nullptr && residual_out == nullptr && x_sumsq == nullptr, EXL3_ERR_ARG,
                  "exl3_gemv_fused: SWIGLU takes one member and no residual or x_sumsq");
+  } else {
+    EXL3_REQUIRE(!residual && !residual_out && !w && !x_sumsq, EXL3_ERR_ARG,
+                 "exl3_gemv_fused: ROTATE takes no residual, residual_out, w or x_sumsq");
   }
-  const GemvPrologueArgs pro{prologue == EXL3_PROLOGUE_RMSNORM ? kProNorm : kProSwiglu,
-                             x, residual, residual_out, w, suh, eps, x_sumsq, y_residual, y_sumsq};
+  const GemvPrologueArgs pro{prologue == EXL3_PROLOGUE_RMSNORM  ? kProNorm
+                             : prologue == EXL3_PROLOGUE_SWIGLU ? kProSwiglu
+                                                                : kProRot,
+                             x, residual, residual_out, xn_out, w, suh, eps, x_sumsq, y_residual, y_sumsq};
   return gemv_run(nullptr, pro, trellis, n_members, member_n, k, K, cb, svh, bias, y, out_dtype, rows, flags,
                   workspace, workspace_bytes, 0, stream);
 }

@@ -22,9 +22,10 @@ struct GemvArgs {
   int k, KT, rows, n_total, S, kt_per_split;
   // input prologue (kProNone: xh is the rotated input)
   int pro;
-  const uint16_t* px;         // kProNorm: x (rows, k); kProSwiglu: gate | up (rows, 2k)
+  const uint16_t* px;         // kProNorm, kProRot: x (rows, k); kProSwiglu: gate | up (rows, 2k)
   const uint16_t* pres;       // kProNorm: residual (rows, k) or null
   uint16_t* pres_out;         // kProNorm: h = x + residual (rows, k) or null
+  uint16_t* pxn_out;          // kProNorm: the norm's output xn (rows, k) or null
   const uint16_t* pw;         // kProNorm: RMSNorm weight (k)
   float eps;
   const uint16_t* psuh;       // input signs (n_members, k)
@@ -34,7 +35,7 @@ struct GemvArgs {
   double* ess;                // (rows, n_total / 128) or null
 };
 
-enum Prologue : int { kProNone = 0, kProNorm = 1, kProSwiglu = 2 };
+enum Prologue : int { kProNone = 0, kProNorm = 1, kProSwiglu = 2, kProRot = 3 };
 
 constexpr int kMaxRows = 16;
 constexpr int kBufferFlags = 0x00020000;   // raw buffer descriptor word 3 (32-bit data, no swizzle) for gfx950

@@ -115,6 +115,9 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const uint16_t* __r
     load_run_words(1, w0, wp0);
     load_run_words(2, w1, wp1);
     store_run(0, 0, w, wp);
+    // one k-step (k <= 64): the padded steps also read the second half, which no step writes; fill it with
+    // zero weights (step 1 lies past the matrix) so that LDS left over from earlier kernels is never read
+    if (nsteps == 1) store_run(1, 1, w, wp);
   } else {
     load_A(0, Aring[0]);
     load_A(1, Aring[1]);
@@ -124,7 +127,8 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const uint16_t* __r
   // The two roles run separate loops with one barrier per step each (same count), so the compiler's wait
   // analysis of one role never sees the other role's loads. The step count is padded to a multiple of three
   // (the MFMA loop's unroll): padded steps decode nothing and contract zero activations (k past the matrix
-  // reads zeros) with the finite weights still in LDS, which adds exactly zero.
+  // reads zeros) with finite weights in LDS (an earlier step's, or the zeros written above), adding exactly
+  // zero.
   const int nsteps_pad = (nsteps + 2) / 3 * 3;
   if (decoder) {
     for (int s = 0; s < nsteps_pad; ++s) {

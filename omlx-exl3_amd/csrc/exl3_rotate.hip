@@ -162,6 +162,12 @@ extern "C" int exl3_rotate(const void* x, int x_dtype, const uint16_t* suh, int 
   EXL3_REQUIRE(x_dtype >= 0 && x_dtype <= 2, EXL3_ERR_ARG, "exl3_rotate: bad x_dtype %d", x_dtype);
   EXL3_REQUIRE(aligned(x, 16) && aligned(suh, 16) && aligned(xh, 16), EXL3_ERR_ARG,
                "exl3_rotate: x, suh and xh must be 16-byte aligned");
+  {
+    const size_t xb = (size_t)rows * k * (x_dtype == kF32 ? 4 : 2);
+    const size_t hb = (size_t)n_members * rows * k * 2;
+    EXL3_REQUIRE(!overlaps(xh, hb, x, xb) && !overlaps(xh, hb, suh, (size_t)n_members * k * 2), EXL3_ERR_ARG,
+                 "exl3_rotate: xh must not overlap x or suh");
+  }
   hipStream_t st = static_cast<hipStream_t>(stream);
   const dim3 grid((unsigned)((k + 2047) / 2048), (unsigned)rows);
   if (x_dtype == kF16) rot_kernel<kF16><<<grid, 256, 0, st>>>(x, suh, n_members, rows, k, xh);
@@ -186,6 +192,21 @@ extern "C" int exl3_rmsnorm_rotate(const void* x, const void* residual, void* re
                    (!xh || aligned(xh, 16)),
                EXL3_ERR_ARG, "exl3_rmsnorm_rotate: buffers must be 16-byte aligned");
   EXL3_REQUIRE(rows <= 65535, EXL3_ERR_ARG, "exl3_rmsnorm_rotate: rows must be <= 65535 (got %d)", rows);
+  {
+    // Every workgroup of a row reads the whole row of x and residual (its sum of squares) while the others
+    // already write their parts of the outputs, so no output may share memory with an input or another output.
+    const size_t rb = (size_t)rows * k * 2, hb = (size_t)n_members * rows * k * 2;
+    const void* outs[3] = {residual_out, xn, xh};
+    const size_t out_bytes[3] = {residual_out ? rb : 0, rb, n_members ? hb : 0};
+    bool bad = false;
+    for (int i = 0; i < 3; ++i) {
+      bad = bad || overlaps(outs[i], out_bytes[i], x, rb) || overlaps(outs[i], out_bytes[i], residual, rb) ||
+            overlaps(outs[i], out_bytes[i], w, (size_t)k * 2);
+      for (int j = i + 1; j < 3; ++j) bad = bad || overlaps(outs[i], out_bytes[i], outs[j], out_bytes[j]);
+    }
+    EXL3_REQUIRE(!bad, EXL3_ERR_ARG,
+                 "exl3_rmsnorm_rotate: residual_out, xn and xh must not overlap x, residual, w or each other");
+  }
   hipStream_t st = static_cast<hipStream_t>(stream);
   const dim3 grid((unsigned)((k + 2047) / 2048), (unsigned)rows);
   if (dtype == kF16)
@@ -203,6 +224,9 @@ extern "C" int exl3_swiglu_rotate(const uint16_t* gu, const uint16_t* suh, int r
   EXL3_REQUIRE(rows >= 1 && rows <= 65535, EXL3_ERR_ARG, "exl3_swiglu_rotate: rows must be 1..65535");
   EXL3_REQUIRE(aligned(gu, 16) && aligned(suh, 16) && aligned(xh, 16), EXL3_ERR_ARG,
                "exl3_swiglu_rotate: buffers must be 16-byte aligned");
+  EXL3_REQUIRE(!overlaps(xh, (size_t)rows * n * 2, gu, (size_t)rows * n * 4) &&
+                   !overlaps(xh, (size_t)rows * n * 2, suh, (size_t)n * 2),
+               EXL3_ERR_ARG, "exl3_swiglu_rotate: xh must not overlap gu or suh");
   hipStream_t st = static_cast<hipStream_t>(stream);
   const dim3 grid((unsigned)((n + 2047) / 2048), (unsigned)rows);
   swiglu_rot_kernel<<<grid, 256, 0, st>>>(gu, suh, rows, n, xh);

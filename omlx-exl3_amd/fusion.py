@@ -1,147 +1,345 @@
 # SPDX-License-Identifier: Apache-2.0
-"""Decode-path fusion of EXL3 input rotations into the kernels that produce their inputs (mirrors
-src/omlx/exl3/fusion.py of the reference, for PyTorch modules).
+"""Decode-step fusion for EXL3 decoders: the element-wise work between a layer's GEMVs runs inside the GEMV
+launches (the prologues and epilogues of exl3_gemv_fused).
 
-Every EXL3 linear consumes xh = had128(x * suh) / sqrt(128). Unfused, a decode step pays one rotation
-launch per linear or sibling group on top of the producer's own kernel. For rows <= MAX_GEMV_ROWS:
+A pre-norm decoder layer computes
 
-  RMSNorm -> EXL3 consumers   input_layernorm -> q/k/v, post_attention_layernorm -> gate/up, the final
-                              norm -> lm_head: one kernel writes the norm output (other readers still
-                              get it) and every consumer's rotated input, grouped or not
-  SwiGLU -> down_proj         down_proj's GEMV forms its rotated input from the gate/up GEMV output
-                              inside its own launch (no SwiGLU launch)
+    h1 = h  + mixer(norm1(h))          mixer: self_attn (q_proj, k_proj, v_proj -> o_proj) or
+    h2 = h1 + mlp(norm2(h1))                  linear_attn (in_proj_qkv, in_proj_z -> out_proj)
+    mlp(x) = down_proj(silu(gate_proj(x)) * up_proj(x))
 
-Priming is keyed on the identity of the norm's output tensor: a consumer that receives any other tensor
-(a view, a cast) computes the rotation itself, so every call path stays correct. Modules keep their
-classes' behaviour for prefill (rows > MAX_GEMV_ROWS); the fused classes are subclasses swapped in per
-instance, so isinstance checks elsewhere still hold.
+(transformers' Llama / Mistral / Qwen2 / Qwen3 decoder layers; the reference fuses the same layers,
+src/omlx/exl3/fusion.py:108-132, with the public entry point `fuse_decode(model) -> counts` kept here).
+fuse_decode binds a DecodeStep to every such layer whose projections are EXL3Linear layers, whose norms are
+plain RMSNorms (w * x / rms) with an fp16 / bf16 weight of a multiple of 128 elements, and whose gate and up
+projections form one sibling group. For rows <= MAX_GEMV_ROWS with fp16 activations a step is four library
+launches besides the mixer's own kernels:
 
-Model shape expected (Llama / Qwen style): decoder layers with `input_layernorm`,
-`post_attention_layernorm`, `self_attn.{q,k,v}_proj`, `mlp.{gate,up,down}_proj`; the output head as
-`lm_head` beside `model.norm`.
+  1. the mixer's input projections with norm1 and the input rotations in the GEMV prologue (one launch per
+     consumer: a sibling group or a single linear); the first launch also writes xn = norm1(h), the tensor
+     handed to the mixer, and the projections the mixer calls on xn are served these outputs;
+  2. the output projection (called by the mixer) with its input rotation in the prologue and h added in
+     the epilogue, which also writes the 128-column block sums of squares of h1;
+  3. gate/up with norm2 in the prologue, its statistics taken from those sums (no second pass over h1);
+  4. down with silu(gate) * up and its rotation in the prologue, h1 added in the epilogue, which writes
+     h2's block sums for the next layer's step 1 (used when that step receives exactly h2).
+
+The unfused form of a layer is nine launches (norm + rotations, GEMV; rotation, GEMV; add; norm + rotations,
+GEMV; SwiGLU + rotation, GEMV; add). DecodeStep(form="separate") runs it with this library's separate
+kernels and gives the same bits (the prologues compute what exl3_rmsnorm_rotate, exl3_swiglu_rotate and
+exl3_rotate write; the epilogue add rounds as torch's fp16 add). bf16 activations take the separate form.
+Prefill rows, ENABLED = False, and layers of any other shape run the model's own forward.
+
+The final norm before an EXL3 output head: the norm and the head's input rotation in one launch (primed into
+the head), then the head's GEMV.
+
+Every tensor handed to model code holds its values, and served or primed results match only the exact tensor
+state they were made for (EXL3Linear.serve / prime), so model code that reads xn, reshapes it or calls a
+projection on anything else stays correct. The mixer must return its output projection's result as it is (as
+attention and linear attention do): the residual is already inside it, so a mixer that changes that result
+is detected and raises.
 """
 from __future__ import annotations
+
+import inspect
 
 import torch
 from torch import nn
 
-from .kernels import MAX_GEMV_ROWS, norm_rot
-from .linear import EXL3Linear
+from .kernels import MAX_GEMV_ROWS, norm_rot, swiglu_rot
+from .linear import EXL3Linear, EXL3SiblingGroup, _Slot
 
-_fused_classes: dict = {}
-ENABLED = True          # runtime switch (benchmarks): False makes the fused modules behave like their bases
+ENABLED = True          # runtime switch (benchmarks, A/B tests): False runs every fused module's own forward
 
+# (mixer attribute, its input projections, its output projection)
+MIXERS = (("self_attn", ("q_proj", "k_proj", "v_proj"), "o_proj"),
+          ("linear_attn", ("in_proj_qkv", "in_proj_z"), "out_proj"))
 
-class _Consumers:
-    """The EXL3 consumers (sibling groups or single linears) of one norm output, primed together
-    (fusion.py:32-48)."""
-
-    def __init__(self, consumers: list):
-        self.consumers = consumers
-        self.nms = [c.rot_suh.shape[0] for c in consumers]
-        self.rot_suh = torch.cat([c.rot_suh for c in consumers]).contiguous() if len(consumers) > 1 \
-            else consumers[0].rot_suh
-
-    def prime(self, x: torch.Tensor, xh: torch.Tensor):
-        if len(self.consumers) == 1:
-            self.consumers[0].prime(x, xh)
-            return
-        o = 0
-        for c, nm in zip(self.consumers, self.nms):
-            c.prime(x, xh[o:o + nm])
-            o += nm
+# RMSNorm classes computed as w * (x / rms(x)) (the kernels' form). Variants scaling by (1 + w), such as
+# Gemma's or Qwen3-Next's, are deliberately absent.
+PLAIN_RMSNORMS = ("RMSNorm", "LlamaRMSNorm", "MistralRMSNorm", "Qwen2RMSNorm", "Qwen3RMSNorm")
 
 
-def _norm_eps(norm: nn.Module, dtype: torch.dtype) -> float:
+def _rms_weight(norm: nn.Module) -> torch.Tensor | None:
+    """The weight of a plain RMSNorm the kernels can compute, else None."""
+    if not (type(norm) is nn.RMSNorm or type(norm).__name__ in PLAIN_RMSNORMS[1:]):   # subclasses may rescale
+        return None
+    w = getattr(norm, "weight", None)
+    if not isinstance(w, torch.Tensor) or w.dim() != 1 or w.shape[0] % 128 or \
+            w.dtype not in (torch.float16, torch.bfloat16):
+        return None
+    return w
+
+
+def _rms_eps(norm: nn.Module, dtype: torch.dtype) -> float:
     eps = getattr(norm, "eps", None)
+    if eps is None:
+        eps = getattr(norm, "variance_epsilon", None)         # transformers' RMSNorm classes
     return float(torch.finfo(dtype).eps) if eps is None else float(eps)
 
 
-def _fused_norm_class(base):
-    if ("norm", base) not in _fused_classes:
-        class FusedNorm(base):
-            def forward(self, x):
-                rows = x.numel() // x.shape[-1]
-                if rows > MAX_GEMV_ROWS or not ENABLED:
-                    return base.forward(self, x)
-                target = self.__dict__["_exl3_target"]
-                xn, xh = norm_rot(x.reshape(rows, x.shape[-1]).contiguous(), self.weight,
-                                  _norm_eps(self, x.dtype), target.rot_suh)
-                xn = xn.reshape(x.shape)
-                target.prime(xn, xh)
-                return xn
-
-        FusedNorm.__name__ = FusedNorm.__qualname__ = base.__name__
-        _fused_classes[("norm", base)] = FusedNorm
-    return _fused_classes[("norm", base)]
+def _consumer(lin) -> EXL3Linear | EXL3SiblingGroup | None:
+    if not isinstance(lin, EXL3Linear):
+        return None
+    return lin._group if lin._group is not None else lin
 
 
-def _fused_mlp_class(base):
-    if ("mlp", base) not in _fused_classes:
-        class FusedMLP(base):
-            def forward(self, x):
-                rows = x.numel() // x.shape[-1]
-                if rows > MAX_GEMV_ROWS or not ENABLED:
-                    return base.forward(self, x)
-                gu = self.gate_proj._group.gemv(x, torch.float16)       # (rows, 2 * hidden): [gate | up]
-                y = self.down_proj.gemv_swiglu(gu, x.dtype)
-                return y.reshape(x.shape[:-1] + (y.shape[-1],))
-
-        FusedMLP.__name__ = FusedMLP.__qualname__ = base.__name__
-        _fused_classes[("mlp", base)] = FusedMLP
-    return _fused_classes[("mlp", base)]
-
-
-def _consumers(module, names) -> list | None:
-    """Distinct EXL3 consumers (group, else the linear itself) of the named linears, in order
-    (fusion.py:86-96)."""
+def _consumers(module: nn.Module | None, names) -> list | None:
+    """The distinct EXL3 consumers (sibling group, else the linear) of the named projections, in order;
+    None unless every one is an EXL3Linear."""
+    if module is None:
+        return None
     out = []
     for n in names:
-        lin = getattr(module, n, None) if module is not None else None
-        if not isinstance(lin, EXL3Linear):
+        c = _consumer(getattr(module, n, None))
+        if c is None:
             return None
-        c = lin._group if lin._group is not None else lin
         if all(c is not o for o in out):
             out.append(c)
     return out
 
 
-def _fuse_norm(norm, consumers) -> bool:
-    """Eligibility (fusion.py:99-105): an RMSNorm with an fp16 / bf16 weight whose size the rotation
-    kernel takes (a multiple of 128)."""
-    w = getattr(norm, "weight", None)
-    if not consumers or not isinstance(norm, nn.RMSNorm) or w is None or w.dim() != 1 \
-            or w.shape[0] % 128 or w.dtype not in (torch.bfloat16, torch.float16):
+def _returns_tuple(fn) -> bool:
+    """Whether a layer's forward is annotated to return a tuple (older transformers layers return
+    (hidden_states, ...)); a tensor otherwise."""
+    try:
+        ann = inspect.signature(fn).return_annotation
+    except (TypeError, ValueError):
         return False
-    norm.__dict__["_exl3_target"] = _Consumers(consumers)       # plain attribute: not a child module
-    norm.__class__ = _fused_norm_class(type(norm))
-    return True
+    return "tuple" in str(ann).lower()
 
 
-def fuse_decode(model: nn.Module) -> dict[str, int]:
-    """Install the decode-path fusions on every eligible decoder layer and the output head
-    (fusion.py:108-132). Returns how many norms, MLPs and heads were fused."""
-    counts = {"norm": 0, "mlp": 0, "head": 0}
-    for _, layer in model.named_modules():
-        if not all(hasattr(layer, k) for k in ("input_layernorm", "post_attention_layernorm", "mlp")):
-            continue
-        first = _consumers(getattr(layer, "self_attn", None), ("q_proj", "k_proj", "v_proj"))
-        counts["norm"] += _fuse_norm(layer.input_layernorm, first)
+class _StreamSums:
+    """The residual stream's 128-block sums of squares, as the last down-projection epilogue wrote them, for
+    the next layer's input norm (only when that layer receives exactly the tensor they describe)."""
+
+    def __init__(self):
+        self.slot = _Slot()
+
+    def put(self, h: torch.Tensor, sums: torch.Tensor):
+        self.slot.put(h, sums)
+
+    def take(self, h: torch.Tensor) -> torch.Tensor | None:
+        return self.slot.take(h)
+
+
+class DecodeStep:
+    """The decode step of one pre-norm decoder layer (module docstring), installed as the layer's forward."""
+
+    def __init__(self, layer: nn.Module, mixer_name: str, in_names, out_name: str, sums: _StreamSums,
+                 form: str = "prologue"):
+        if form not in ("prologue", "separate"):
+            raise ValueError(f"DecodeStep: unknown form {form!r}")
+        self.layer = layer
+        self.mixer = getattr(layer, mixer_name)
+        self.in_consumers = _consumers(self.mixer, in_names)
+        self.out_proj: EXL3Linear = getattr(self.mixer, out_name)
+        self.norm1, self.norm2 = layer.input_layernorm, layer.post_attention_layernorm
         mlp = layer.mlp
-        second = _consumers(mlp, ("gate_proj", "up_proj"))
-        counts["norm"] += _fuse_norm(layer.post_attention_layernorm, second)
-        gu = mlp.gate_proj._group if second else None
-        down = getattr(mlp, "down_proj", None)
-        if gu is not None and len(gu.members) == 2 and gu.members[0] is mlp.gate_proj \
-                and gu.members[1] is mlp.up_proj and gu.ns[0] == gu.ns[1] \
-                and isinstance(down, EXL3Linear) and "bias" not in down:
-            down._prepare()
-            mlp.__class__ = _fused_mlp_class(type(mlp))
-            counts["mlp"] += 1
+        self.gate_up: EXL3SiblingGroup = mlp.gate_proj._group
+        self.down: EXL3Linear = mlp.down_proj
+        self.hidden = self.norm1.weight.shape[0]
+        self.sums = sums
+        self.form = form
+        self.base = layer.forward                     # the model's own forward (bound method)
+        self.tuple_out = _returns_tuple(self.base)
+        sig = None
+        try:
+            sig = inspect.signature(self.base)
+        except (TypeError, ValueError):
+            pass
+        self._sig = sig
+        self.down._prepare()
+        self.out_proj._prepare()
+
+    @staticmethod
+    def eligible(layer: nn.Module):
+        """(mixer name, input projection names, output projection name) when the layer has the fusable
+        shape, else None."""
+        if not all(hasattr(layer, a) for a in ("input_layernorm", "post_attention_layernorm", "mlp")):
+            return None
+        if type(layer).forward is nn.Module.forward:      # a container without a forward of its own
+            return None
+        for mixer_name, in_names, out_name in MIXERS:
+            mixer = getattr(layer, mixer_name, None)
+            if mixer is None:
+                continue
+            if _consumers(mixer, in_names) is None or not isinstance(getattr(mixer, out_name, None), EXL3Linear):
+                return None
+            w1, w2 = _rms_weight(layer.input_layernorm), _rms_weight(layer.post_attention_layernorm)
+            mlp = layer.mlp
+            gate, up, down = (getattr(mlp, n, None) for n in ("gate_proj", "up_proj", "down_proj"))
+            if w1 is None or w2 is None or not all(isinstance(m, EXL3Linear) for m in (gate, up, down)):
+                return None
+            grp = gate._group
+            if grp is None or grp is not up._group or grp.members != [gate, up] or grp.ns[0] != grp.ns[1]:
+                return None
+            if down.in_features != gate.out_features or getattr(mixer, out_name).out_features != w1.shape[0]:
+                return None
+            return mixer_name, in_names, out_name
+        return None
+
+    def _mixer_kwargs(self, hidden_states, args, kwargs) -> dict:
+        """The layer call's arguments after hidden_states, as keywords for the mixer (the layer passes them
+        on by name, as transformers' layers do)."""
+        if not args:
+            return dict(kwargs)
+        if self._sig is None:
+            raise TypeError("DecodeStep: positional layer arguments need an inspectable forward signature")
+        bound = self._sig.bind(hidden_states, *args, **kwargs)
+        names = list(self._sig.parameters)
+        out = {}
+        for name, val in bound.arguments.items():
+            if name == names[0]:
+                continue
+            if self._sig.parameters[name].kind is inspect.Parameter.VAR_KEYWORD:
+                out.update(val)
+            else:
+                out[name] = val
+        return out
+
+    def __call__(self, hidden_states: torch.Tensor, *args, **kwargs):
+        rows = hidden_states.numel() // hidden_states.shape[-1]
+        dt = hidden_states.dtype
+        if not ENABLED or rows > MAX_GEMV_ROWS or dt not in (torch.float16, torch.bfloat16) or \
+                hidden_states.shape[-1] != self.hidden or torch.is_grad_enabled() and hidden_states.requires_grad:
+            return self.base(hidden_states, *args, **kwargs)
+        mk = self._mixer_kwargs(hidden_states, args, kwargs)
+        if self.form == "prologue" and dt == torch.float16:
+            h2 = self._prologue(hidden_states, rows, mk)
+        else:
+            h2 = self._separate(hidden_states, rows, mk)
+        return (h2,) if self.tuple_out else h2
+
+    def _mixer_out(self, out) -> torch.Tensor:
+        return out[0] if isinstance(out, tuple) else out
+
+    def _prologue(self, hs: torch.Tensor, rows: int, mk: dict) -> torch.Tensor:
+        k = self.hidden
+        dt = hs.dtype
+        h = hs.reshape(rows, k)
+        if not h.is_contiguous():
+            h = h.contiguous()
+        ss = self.sums.take(hs)
+        n1 = self.norm1
+        xn = torch.empty_like(h)
+        xn_v = xn.view(hs.shape)
+        for i, c in enumerate(self.in_consumers):   # 1: input projections, norm1 inside the launch
+            y = c.gemv_rmsnorm(h, None, n1.weight, _rms_eps(n1, dt), dt, x_sumsq=ss, xn_out=xn if i == 0 else None)
+            c.serve(xn_v, y if isinstance(c, EXL3SiblingGroup) else y.reshape(hs.shape[:-1] + (c.out_features,)))
+        ss1 = torch.empty((rows, k // 128), dtype=torch.float64, device=h.device)
+        self.out_proj.arm_residual(h, ss1)              # 2: o_proj's epilogue adds h
+        try:
+            o = self._mixer_out(self.mixer(xn_v, **mk))
+        finally:
+            h1 = self.out_proj.take_armed_output()
+            for c in self.in_consumers:                 # nothing served stays behind
+                c._served.clear()
+        if h1 is None or o.data_ptr() != h1.data_ptr() or o.numel() != h1.numel():
+            raise RuntimeError("DecodeStep: the mixer did not return its output projection's result as it is; "
+                               "this layer cannot take the residual add in that projection's epilogue "
+                               "(fuse_decode(model, form='separate') avoids it)")
+        h1 = h1.reshape(rows, k)
+        n2 = self.norm2
+        gu = self.gate_up.gemv_rmsnorm(h1, None, n2.weight, _rms_eps(n2, dt), torch.float16, x_sumsq=ss1)   # 3
+        ss2 = torch.empty((rows, k // 128), dtype=torch.float64, device=h.device)
+        h2 = self.down.gemv_swiglu(gu, dt, y_residual=h1, y_sumsq=ss2).view(hs.shape)                     # 4
+        self.sums.put(h2, ss2)
+        return h2
+
+    def _separate(self, hs: torch.Tensor, rows: int, mk: dict) -> torch.Tensor:
+        k = self.hidden
+        dt = hs.dtype
+        h = hs.reshape(rows, k)
+        if not h.is_contiguous():
+            h = h.contiguous()
+        n1, n2 = self.norm1, self.norm2
+        suh = torch.cat([c.rot_suh for c in self.in_consumers]) if len(self.in_consumers) > 1 \
+            else self.in_consumers[0].rot_suh
+        xn, xh = norm_rot(h, n1.weight, _rms_eps(n1, dt), suh)
+        xn_v = xn.view(hs.shape)
+        o = 0
+        for c in self.in_consumers:
+            nm = c.rot_suh.shape[0]
+            c.prime(xn_v, xh[o:o + nm])
+            o += nm
+        try:
+            out = self._mixer_out(self.mixer(xn_v, **mk))
+        finally:
+            for c in self.in_consumers:
+                c._primed.clear()
+        xn2, xh2, h1 = norm_rot(out.reshape(rows, k).contiguous(), n2.weight, _rms_eps(n2, dt),
+                                self.gate_up.rot_suh, residual=h)
+        self.gate_up.prime(xn2, xh2)
+        gu = self.gate_up.gemv(xn2, torch.float16)
+        d = self.down.gemv_rotated(swiglu_rot(gu, self.down._suh), dt, self.down._bias_for(dt))
+        return (h1 + d.reshape(rows, k)).view(hs.shape)
+
+
+class HeadNorm:
+    """The final norm before an EXL3 output head, installed as the norm's forward: for decode rows the norm
+    and the head's input rotation in one launch, primed into the head."""
+
+    def __init__(self, norm: nn.Module, head: EXL3Linear):
+        self.norm, self.head = norm, head
+        self.base = norm.forward
+        head._prepare()
+
+    def __call__(self, x: torch.Tensor) -> torch.Tensor:
+        rows = x.numel() // x.shape[-1]
+        if not ENABLED or rows > MAX_GEMV_ROWS or x.dtype != self.norm.weight.dtype:
+            return self.base(x)
+        xn, xh = norm_rot(x.reshape(rows, x.shape[-1]).contiguous(), self.norm.weight,
+                          _rms_eps(self.norm, x.dtype), self.head.rot_suh)
+        xn = xn.view(x.shape)
+        self.head.prime(xn, xh)
+        return xn
+
+
+def _head_pair(model: nn.Module):
+    """(final norm, EXL3 output head) of a causal LM laid out as model.norm + lm_head, or None."""
+    head = getattr(model, "lm_head", None)
     inner = getattr(model, "model", None)
-    if inner is not None and hasattr(inner, "norm"):
-        counts["head"] += _fuse_norm(inner.norm, _consumers(model, ("lm_head",)))
+    norm = getattr(inner, "norm", None) if inner is not None else None
+    if norm is None:
+        norm = getattr(model, "norm", None)
+    if not isinstance(head, EXL3Linear) or head._group is not None or norm is None or _rms_weight(norm) is None:
+        return None
+    return norm, head
+
+
+def fuse_decode(model: nn.Module, form: str = "prologue") -> dict[str, int]:
+    """Install the decode-step fusion on every eligible decoder layer and the output head (module docstring).
+    Returns counts: decoder layers bound ("layer"), norms folded into launches ("norm"), MLPs ("mlp") and
+    heads ("head"). Calling it again replaces earlier bindings."""
+    unfuse(model)
+    counts = {"layer": 0, "norm": 0, "mlp": 0, "head": 0}
+    sums = _StreamSums()
+    for _, layer in model.named_modules():
+        spec = DecodeStep.eligible(layer)
+        if spec is None:
+            continue
+        layer.forward = DecodeStep(layer, *spec, sums=sums, form=form)
+        counts["layer"] += 1
+        counts["norm"] += 2
+        counts["mlp"] += 1
+    pair = _head_pair(model)
+    if pair is not None:
+        norm, head = pair
+        norm.forward = HeadNorm(norm, head)
+        counts["norm"] += 1
+        counts["head"] += 1
     return counts
 
 
-__all__ = ["fuse_decode", "ENABLED"]
+def unfuse(model: nn.Module) -> int:
+    """Remove what fuse_decode installed; returns how many modules it restored."""
+    n = 0
+    for _, m in model.named_modules():
+        if isinstance(m.__dict__.get("forward"), (DecodeStep, HeadNorm)):
+            del m.forward
+            n += 1
+    return n
+
+
+__all__ = ["fuse_decode", "unfuse", "DecodeStep", "HeadNorm", "ENABLED", "MIXERS", "PLAIN_RMSNORMS"]

@@ -11,13 +11,14 @@ kernels.py:269-270, 465); the C library re-validates and its status becomes an E
 from __future__ import annotations
 
 import ctypes
+import math
 import os
 
 import torch
 
 from ._capi import DTYPE_CODE, Exl3Error, check, lib, ptr, stream_handle
 
-PROLOGUE_NONE, PROLOGUE_RMSNORM, PROLOGUE_SWIGLU = 0, 1, 2      # exl3_gemv_fused input prologues
+PROLOGUE_NONE, PROLOGUE_RMSNORM, PROLOGUE_SWIGLU, PROLOGUE_ROTATE = 0, 1, 2, 3   # exl3_gemv_fused prologues
 MAX_GEMV_ROWS = 8           # rows at or below which EXL3Linear takes the GEMV path (kernels.py:260)
 GEMV_ROWS_LIMIT = 16        # rows one GEMV launch accepts
 GEMV_EXACT, GEMV_FAST, GEMV_TABLE = 0, 1, 2
@@ -31,6 +32,28 @@ def _require(cond: bool, msg: str) -> None:
 def _dev(t: torch.Tensor, name: str) -> None:
     _require(isinstance(t, torch.Tensor) and t.is_cuda, f"{name} must be a tensor on the HIP device")
     _require(t.is_contiguous(), f"{name} must be contiguous")
+
+
+def _overlap(a: torch.Tensor | None, b: torch.Tensor | None) -> bool:
+    """True when two device tensors share a byte of memory."""
+    if a is None or b is None:
+        return False
+    a0, b0 = a.data_ptr(), b.data_ptr()
+    return a0 < b0 + b.numel() * b.element_size() and b0 < a0 + a.numel() * a.element_size()
+
+
+def _check_out(out: torch.Tensor, shape: tuple, dtype: torch.dtype, name: str = "out") -> None:
+    """A caller-provided output: on the device, contiguous, of exactly this shape (element count) and dtype."""
+    _dev(out, name)
+    _require(out.dtype == dtype and out.numel() == math.prod(shape),
+             f"{name} must be {dtype} with {math.prod(shape)} elements {tuple(shape)}, got {out.dtype} {tuple(out.shape)}")
+
+
+def _check_vec(t: torch.Tensor | None, n: int, dtype: torch.dtype, name: str) -> None:
+    if t is None:
+        return
+    _dev(t, name)
+    _require(t.dtype == dtype and t.numel() == n, f"{name} must be {dtype} with {n} elements, got {t.dtype} {t.numel()}")
 
 
 def trellis_words(trellis: torch.Tensor, k: int, n: int, K: int) -> torch.Tensor:
@@ -58,7 +81,7 @@ def decode_wt(trellis: torch.Tensor, k: int, n: int, K: int, cb: int, nt0: int =
     trellis_words(trellis, k, n, K)
     if out is None:
         out = torch.empty((16 * ntc, k), dtype=torch.float16, device=trellis.device)
-    _require(out.dtype == torch.float16 and out.shape == (16 * ntc, k), "decode_wt: bad output tensor")
+    _check_out(out, (16 * ntc, k), torch.float16)
     check(lib().exl3_reconstruct(ptr(trellis), k, n, K, cb, nt0, ntc, ptr(out), stream_handle(trellis.device)),
           "exl3_reconstruct")
     return out
@@ -74,6 +97,9 @@ def rot(x: torch.Tensor, suh: torch.Tensor, out: torch.Tensor | None = None) -> 
     _require(x.dtype in DTYPE_CODE and suh.dtype == torch.float16, "rot: x must be fp16/bf16/fp32, suh fp16")
     if out is None:
         out = torch.empty((nm, rows, k), dtype=torch.float16, device=x.device)
+    else:
+        _check_out(out, (nm, rows, k), torch.float16)
+        _require(not (_overlap(out, x) or _overlap(out, suh2)), "rot: out must not overlap x or suh")
     check(lib().exl3_rotate(ptr(x), DTYPE_CODE[x.dtype], ptr(suh2), nm, rows, k, ptr(out), stream_handle(x.device)),
           "exl3_rotate")
     return out
@@ -102,6 +128,10 @@ def norm_rot(x: torch.Tensor, w: torch.Tensor, eps: float, suh: torch.Tensor | N
         _require(residual.shape == x.shape and residual.dtype == x.dtype, "norm_rot: residual like x")
         if residual_out is None:
             residual_out = torch.empty_like(x)
+        _check_out(residual_out, tuple(x.shape), x.dtype, "residual_out")
+        # each row is spread over several workgroups that read all of x and residual while the others write
+        _require(not (_overlap(residual_out, x) or _overlap(residual_out, residual) or _overlap(residual_out, w)),
+                 "norm_rot: residual_out must not overlap x, residual or w (not in place)")
     check(lib().exl3_rmsnorm_rotate(ptr(x), ptr(residual), ptr(residual_out), ptr(w), DTYPE_CODE[x.dtype],
                                     float(eps), ptr(suh), nm, rows, k, ptr(xn), ptr(xh), stream_handle(x.device)),
           "exl3_rmsnorm_rotate")
@@ -120,6 +150,9 @@ def swiglu_rot(gu: torch.Tensor, suh: torch.Tensor, out: torch.Tensor | None = N
     _require(gu.dtype == torch.float16 and suh.dtype == torch.float16 and suh.numel() == n, "swiglu_rot: fp16")
     if out is None:
         out = torch.empty((1, rows, n), dtype=torch.float16, device=gu.device)
+    else:
+        _check_out(out, (1, rows, n), torch.float16)
+        _require(not (_overlap(out, gu) or _overlap(out, suh)), "swiglu_rot: out must not overlap gu or suh")
     check(lib().exl3_swiglu_rotate(ptr(gu), ptr(suh), rows, n, ptr(out), stream_handle(gu.device)),
           "exl3_swiglu_rotate")
     return out
@@ -170,11 +203,11 @@ class TrellisGemvPlan:
             self._tr_c = (ctypes.c_void_p * 3)(*(list(key) + [key[0]] * (3 - len(key))))
             self._tr_key = key
             self._tr_refs = list(trellises)
-        if bias is not None:
-            _require(bias.dtype == self.out_dtype and bias.numel() == self.n and bias.is_contiguous(),
-                     "bias must be contiguous, out_dtype, n elements")
+        _check_vec(bias, self.n, self.out_dtype, "bias")
         if out is None:
             out = torch.empty((self.rows, self.n), dtype=self.out_dtype, device=device)
+        else:
+            _check_out(out, (self.rows, self.n), self.out_dtype)
         return out
 
     def __call__(self, xh: torch.Tensor, trellises: list[torch.Tensor], bias: torch.Tensor | None = None,
@@ -193,23 +226,25 @@ class TrellisGemvPlan:
 
     def fused(self, prologue: int, x: torch.Tensor, trellises: list[torch.Tensor], *,
               residual: torch.Tensor | None = None, residual_out: torch.Tensor | None = None,
-              weight: torch.Tensor | None = None, eps: float = 0.0, x_sumsq: torch.Tensor | None = None,
+              xn_out: torch.Tensor | None = None, weight: torch.Tensor | None = None, eps: float = 0.0, x_sumsq: torch.Tensor | None = None,
               suh: torch.Tensor | None = None, bias: torch.Tensor | None = None,
               y_residual: torch.Tensor | None = None, y_sumsq: torch.Tensor | None = None,
               out: torch.Tensor | None = None) -> torch.Tensor:
         """The GEMV with its neighbouring element-wise steps in the same launch (exl3_gemv_fused).
         prologue PROLOGUE_NONE: x is the rotated input (n_members, rows, k); PROLOGUE_RMSNORM: x (rows, k)
         [+ residual, h to residual_out], RMSNorm with weight / eps (x_sumsq: the block sums of squares of x
-        from a previous call, no residual), rotations by suh (n_members, k); PROLOGUE_SWIGLU: x = [gate | up]
+        from a previous call, no residual; the norm's output to xn_out when given), rotations by suh
+        (n_members, k); PROLOGUE_SWIGLU: x = [gate | up]
         (rows, 2k), suh (k). Epilogue (fp16 output): y += y_residual; y_sumsq (rows, n/128) fp64 receives
         the block sums of squares of y."""
         _dev(x, "x")
         _require(x.dtype == torch.float16 and x.is_contiguous(), "x must be contiguous fp16")
         want = {PROLOGUE_NONE: self.nsub * self.rows * self.k, PROLOGUE_RMSNORM: self.rows * self.k,
-                PROLOGUE_SWIGLU: 2 * self.rows * self.k}.get(prologue)
+                PROLOGUE_SWIGLU: 2 * self.rows * self.k, PROLOGUE_ROTATE: self.rows * self.k}.get(prologue)
         _require(want is not None and x.numel() == want, f"x has {x.numel()} elements, prologue {prologue} wants {want}")
         for t, name, n, dt in ((residual, "residual", self.rows * self.k, torch.float16),
                                (residual_out, "residual_out", self.rows * self.k, torch.float16),
+                               (xn_out, "xn_out", self.rows * self.k, torch.float16),
                                (weight, "weight", self.k, torch.float16),
                                (x_sumsq, "x_sumsq", self.rows * (self.k // 128), torch.float64),
                                (suh, "suh", (1 if prologue == PROLOGUE_SWIGLU else self.nsub) * self.k, torch.float16),
@@ -218,9 +253,13 @@ class TrellisGemvPlan:
             if t is not None:
                 _dev(t, name)
                 _require(t.dtype == dt and t.is_contiguous() and t.numel() == n, f"{name}: contiguous {dt}, {n} elements")
+        for o in (residual_out, xn_out):
+            _require(not (_overlap(o, x) or _overlap(o, residual) or _overlap(o, weight)),
+                     "residual_out / xn_out must not overlap x, residual or weight")
+        _require(not _overlap(residual_out, xn_out), "residual_out and xn_out must not overlap")
         out = self._bind(trellises, bias, out, x.device)
-        rc = lib().exl3_gemv_fused(prologue, ptr(x), ptr(residual), ptr(residual_out), ptr(weight), float(eps),
-                                   ptr(x_sumsq), ptr(suh), self._tr_c, self.nsub, self._ns_c, self.k, self.K, self.cb,
+        rc = lib().exl3_gemv_fused(prologue, ptr(x), ptr(residual), ptr(residual_out), ptr(xn_out), ptr(weight),
+                                   float(eps), ptr(x_sumsq), ptr(suh), self._tr_c, self.nsub, self._ns_c, self.k, self.K, self.cb,
                                    ptr(self.svh), ptr(bias), ptr(out), DTYPE_CODE[self.out_dtype], self.rows,
                                    self.flags, ptr(y_residual), ptr(y_sumsq), ptr(self.workspace),
                                    self.workspace.numel(), stream_handle(x.device))
@@ -235,6 +274,11 @@ class TrellisGemvPlan:
     def swiglu(self, gu: torch.Tensor, suh: torch.Tensor, trellises: list[torch.Tensor], **kw) -> torch.Tensor:
         """fused(PROLOGUE_SWIGLU, ...): the GEMV of rot(silu(gate) * up, suh) with gu = [gate | up]."""
         return self.fused(PROLOGUE_SWIGLU, gu, trellises, suh=suh, **kw)
+
+    def rotate(self, x: torch.Tensor, suh: torch.Tensor, trellises: list[torch.Tensor], **kw) -> torch.Tensor:
+        """fused(PROLOGUE_ROTATE, ...): the GEMV of rot(x, suh_m) per member, the rotation inside the launch
+        (the same values as rot followed by __call__)."""
+        return self.fused(PROLOGUE_ROTATE, x, trellises, suh=suh, **kw)
 
 
 # GEMM solution table of the library-GEMM prefill form: PyTorch TunableOp's CSV, made on MI355X by
@@ -296,10 +340,16 @@ def prefill_gemm(xh: torch.Tensor, trellis: torch.Tensor, k: int, n: int, K: int
     rows = xh.numel() // k
     _require(xh.dtype == torch.float16 and xh.numel() == rows * k, "xh must be fp16 (rows, k)")
     _require(path in ("auto", "fused", "library"), f"prefill_gemm: unknown path {path!r}")
+    _require(out_dtype in DTYPE_CODE, "prefill_gemm: out_dtype fp16, bf16 or fp32")
     trellis_words(trellis, k, n, K)
     svh = svh.to(torch.float16).reshape(-1).contiguous()
+    _check_vec(svh, n, torch.float16, "svh")
+    _check_vec(bias, n, out_dtype, "bias")
     if out is None:
         out = torch.empty((rows, n), dtype=out_dtype, device=xh.device)
+    else:
+        _check_out(out, (rows, n), out_dtype)
+        _require(not _overlap(out, xh), "prefill_gemm: out must not overlap xh")
     if path == "library" or (path == "auto" and rows >= PREFILL_LIBRARY_ROWS):
         wt = torch.empty((n, k), dtype=torch.float16, device=xh.device)
         check(lib().exl3_reconstruct(ptr(trellis), k, n, K, cb, 0, n // 16, ptr(wt), stream_handle(xh.device)),

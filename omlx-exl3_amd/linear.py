@@ -5,9 +5,9 @@ EXL3Linear holds exactly the checkpoint tensors of one ExLlamaV3 linear (trellis
 the mul1 / mcg codebook marker, optional bias) as module buffers, so a strict `load_state_dict` fills it
 like any layer. Forward computes  y = had128( had128(x * suh) @ W_inner ) * svh  (+ bias):
 
-  rows <= MAX_GEMV_ROWS (decode, speculative verify): the input rotation (one kernel, or none when the
-      producer primed it, see fusion.py), then one fused GEMV launch that also reduces, applies the output
-      rotation, svh and the bias, and writes the caller's dtype (kernels.TrellisGemvPlan)
+  rows <= MAX_GEMV_ROWS (decode, speculative verify): one GEMV launch that rotates the input (fp16 input;
+      other dtypes take a rotation launch first, and a primed rotated input is used as it is), reduces,
+      applies the output rotation, svh and the bias, and writes the caller's dtype (kernels.TrellisGemvPlan)
   more rows (prefill, kernels.prefill_gemm): the input rotation, then from kernels.PREFILL_LIBRARY_ROWS
       (every prefill row count by default) the reference's own sequence: W_inner^T reconstructed once, a
       library fp16 GEMM, then the output rotation, svh and bias in one kernel; below it, or with
@@ -15,16 +15,22 @@ like any layer. Forward computes  y = had128( had128(x * suh) @ W_inner ) * svh 
       the output rotation, svh and bias (the fp16 weight matrix is never written to memory)
 
 EXL3SiblingGroup runs same-input siblings (q/k/v, gate/up) as one GEMV launch over their own trellis
-buffers when they share K and codebook; each member returns its slice of the output, served from a
-single-slot cache keyed on the input tensor's identity.
+buffers when they share K and codebook; each member returns its slice of the output, held until every
+member has taken its slice.
 
-Single-thread assumption, as in the reference: priming and the group cache are identity-keyed slots.
+Values computed ahead of a call (a primed rotated input, a served output, the group's outputs) are matched
+to the call's input by the tensor's state: storage address, shape, strides, dtype and version counter.
+The slot keeps the tensor alive, so only that tensor or a view of the same memory with the same layout can
+match, and an in-place write to it (or to any view of it) advances the version and voids the match. A
+call with any other input computes for itself. Single-thread assumption, as in the reference: the slots
+are per module, one value each.
 """
 from __future__ import annotations
 
 import math
 
 import torch
+import torch.nn.functional as F
 from torch import nn
 
 from .kernels import MAX_GEMV_ROWS, PROLOGUE_NONE, TrellisGemvPlan, prefill_gemm, rot
@@ -55,6 +61,33 @@ def had128(v: torch.Tensor, scale: float = _HAD_SCALE) -> torch.Tensor:
         x = torch.stack((a + b, a - b), dim=2)
         h *= 2
     return (x.reshape(shape) * scale)
+
+
+def _state(t: torch.Tensor) -> tuple:
+    """What pins a live tensor's contents: storage address, shape, strides, dtype and version counter."""
+    return (t.data_ptr(), tuple(t.shape), t.stride(), t.dtype, t._version)
+
+
+class _Slot:
+    """One value computed ahead for the next call whose input has exactly `key`'s state (taken once)."""
+
+    __slots__ = ("key", "state", "value")
+
+    def __init__(self):
+        self.clear()
+
+    def clear(self):
+        self.key = self.state = self.value = None
+
+    def put(self, key: torch.Tensor, value):
+        self.key, self.state, self.value = key, _state(key), value
+
+    def take(self, x: torch.Tensor):
+        if self.key is None or _state(x) != self.state:
+            return None
+        v = self.value
+        self.clear()
+        return v
 
 
 _DTYPE_NAMES = {"I16": torch.int16, "F16": torch.float16, "BF16": torch.bfloat16, "F32": torch.float32,
@@ -88,7 +121,10 @@ class EXL3Linear(nn.Module):
         self._group = None
         self._idx = 0
         self._ready = False
-        self._primed = None
+        self._primed = _Slot()          # rotated input for the next call with that input
+        self._served = _Slot()          # output for the next call with that input
+        self._armed = None              # (residual, y_sumsq) for the next decode call's epilogue
+        self._armed_out = None
 
     def __contains__(self, name: str) -> bool:
         return name in self._parts
@@ -144,8 +180,24 @@ class EXL3Linear(nn.Module):
         return self._suh2d
 
     def prime(self, x: torch.Tensor, xh: torch.Tensor):
-        """The next call with exactly this tensor uses xh as its rotated input (fusion.py)."""
-        self._primed = (x, xh)
+        """The next call with this input (same tensor state) uses xh as its rotated input (linear.py:80-82)."""
+        self._primed.put(x, xh)
+
+    def serve(self, x: torch.Tensor, y: torch.Tensor):
+        """The next call with this input (same tensor state) returns y: an output computed ahead, e.g. by a
+        GEMV launch that also formed this input (fusion.py)."""
+        self._served.put(x, y)
+
+    def arm_residual(self, residual: torch.Tensor, y_sumsq: torch.Tensor | None = None):
+        """The next decode call (rows <= MAX_GEMV_ROWS, fp16) returns fp16(y + residual) from its GEMV launch,
+        and writes the result's 128-column block sums of squares to y_sumsq (rows, out_features / 128) fp64
+        when given: the residual add and the next RMSNorm's statistics in the GEMV's epilogue."""
+        self._armed, self._armed_out = (residual, y_sumsq), None
+
+    def take_armed_output(self) -> torch.Tensor | None:
+        """The output of the call that consumed arm_residual (None if no call did); disarms."""
+        out, self._armed, self._armed_out = self._armed_out, None, None
+        return out
 
     def _bias_for(self, dtype: torch.dtype):
         """The bias in the output dtype (cast once per dtype), or None."""
@@ -164,29 +216,50 @@ class EXL3Linear(nn.Module):
                 self.in_features, [self.out_features], self._K, self._cb, self._svh, rows, out_dtype)
         return plan
 
+    def _take_arm(self, rows: int, out_dtype: torch.dtype):
+        """(y_residual, y_sumsq) of an armed residual epilogue for this call, or (None, None)."""
+        if self._armed is None:
+            return None, None
+        y_res, y_ss = self._armed
+        self._armed = None                            # one call takes it
+        if out_dtype != torch.float16 or y_res.dtype != torch.float16 or y_res.numel() != rows * self.out_features:
+            raise ValueError("EXL3Linear: the armed residual epilogue needs an fp16 output and an fp16 residual "
+                             "of the call's shape")
+        return y_res.reshape(rows, self.out_features), y_ss
+
     def gemv_rotated(self, xh: torch.Tensor, out_dtype: torch.dtype, bias: torch.Tensor | None = None,
                      y_residual: torch.Tensor | None = None, y_sumsq: torch.Tensor | None = None) -> torch.Tensor:
         """(rows, out_features) from an already rotated input xh, (1, rows, k) or (rows, k)
         (linear.py:84-92). `bias` (out_dtype, out_features) is added inside the kernel before rounding.
         Epilogue (fp16): y_residual is added to the output and y_sumsq (rows, out_features / 128) fp64
-        receives its block sums of squares, for a following gemv_rmsnorm."""
-        plan = self._plan(xh.shape[-2], out_dtype)
+        receives its block sums of squares, for a following gemv_rmsnorm; without them an armed residual
+        (arm_residual) applies."""
+        rows = xh.shape[-2]
+        armed = y_residual is None and y_sumsq is None and self._armed is not None
+        if armed:
+            y_residual, y_sumsq = self._take_arm(rows, out_dtype)
+        plan = self._plan(rows, out_dtype)
         if y_residual is None and y_sumsq is None:
-            return plan(xh.contiguous(), [self._tr], bias=bias)
-        return plan.fused(PROLOGUE_NONE, xh.contiguous(), [self._tr], bias=bias, y_residual=y_residual,
-                          y_sumsq=y_sumsq)
+            y = plan(xh.contiguous(), [self._tr], bias=bias)
+        else:
+            y = plan.fused(PROLOGUE_NONE, xh.contiguous(), [self._tr], bias=bias, y_residual=y_residual,
+                           y_sumsq=y_sumsq)
+        if armed:
+            self._armed_out = y
+        return y
 
     def gemv_rmsnorm(self, x: torch.Tensor, residual: torch.Tensor | None, weight: torch.Tensor, eps: float,
                      out_dtype: torch.dtype, residual_out: torch.Tensor | None = None,
-                     x_sumsq: torch.Tensor | None = None) -> torch.Tensor:
+                     x_sumsq: torch.Tensor | None = None, xn_out: torch.Tensor | None = None) -> torch.Tensor:
         """(rows, out_features) of this linear applied to rmsnorm(x + residual) * weight, with the residual
         add, norm and input rotation inside the GEMV launch; h = x + residual is written to residual_out
-        when given; x_sumsq: x's block sums of squares from the producing launch (no residual). fp16 x,
-        residual, weight; rows <= MAX_GEMV_ROWS. Equal, bit for bit, to norm_rot followed by gemv_rotated."""
+        and the norm's output to xn_out when given; x_sumsq: x's block sums of squares from the producing
+        launch (no residual). fp16 x, residual, weight; rows <= MAX_GEMV_ROWS. Equal, bit for bit, to
+        norm_rot followed by gemv_rotated."""
         rows = x.numel() // self.in_features
         return self._plan(rows, out_dtype).rmsnorm(x, residual, weight, eps, self._suh2d, [self._tr],
                                                    bias=self._bias_for(out_dtype), residual_out=residual_out,
-                                                   x_sumsq=x_sumsq)
+                                                   x_sumsq=x_sumsq, xn_out=xn_out)
 
     def gemv_swiglu(self, gu: torch.Tensor, out_dtype: torch.dtype, y_residual: torch.Tensor | None = None,
                     y_sumsq: torch.Tensor | None = None) -> torch.Tensor:
@@ -206,7 +279,10 @@ class EXL3Linear(nn.Module):
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if self._group is not None:
-            return self._group(x)[self._idx]
+            return self._group.member_output(x, self._idx)
+        y = self._served.take(x)
+        if y is not None:
+            return y
         self._prepare()
         in_shape, dtype = x.shape, x.dtype
         if x.shape[-1] != self.in_features:
@@ -214,10 +290,19 @@ class EXL3Linear(nn.Module):
         rows = x.numel() // self.in_features
         bias = self._bias_for(dtype)
         if rows <= MAX_GEMV_ROWS:
-            primed, self._primed = self._primed, None
-            xh = primed[1] if primed is not None and primed[0] is x else \
-                rot(x.reshape(rows, self.in_features).contiguous(), self._suh2d)
-            y = self.gemv_rotated(xh, dtype, bias)
+            xh = self._primed.take(x)
+            if xh is None and dtype == torch.float16:
+                # the input rotation inside the GEMV launch (exl3_gemv_fused, ROTATE prologue)
+                armed = self._armed is not None
+                y_res, y_ss = self._take_arm(rows, dtype)
+                y = self._plan(rows, dtype).rotate(x.reshape(rows, self.in_features).contiguous(), self._suh2d,
+                                                   [self._tr], bias=bias, y_residual=y_res, y_sumsq=y_ss)
+                if armed:
+                    self._armed_out = y
+            else:
+                if xh is None:
+                    xh = rot(x.reshape(rows, self.in_features).contiguous(), self._suh2d)
+                y = self.gemv_rotated(xh, dtype, bias)
         else:
             xh = rot(x.reshape(rows, self.in_features).contiguous(), self._suh2d).reshape(rows, self.in_features)
             y = self._prefill(xh, dtype, bias)
@@ -242,9 +327,11 @@ class EXL3SiblingGroup:
         self.svh = torch.cat([m._svh for m in members]).contiguous()
         self.trs = [m._tr for m in members]
         self.plans: dict = {}
-        self._cache_x = None
-        self._cache_out = None
-        self._primed = None
+        self._primed = _Slot()          # rotated input (n_members, rows, k) for the next call with that input
+        self._served = _Slot()          # concatenated outputs for the next call with that input
+        self._outs = None               # the last call's per-member outputs, until every member took its own
+        self._outs_state = None
+        self._outs_taken: set = set()
         for i, m in enumerate(members):
             m._group, m._idx = self, i
 
@@ -262,8 +349,13 @@ class EXL3SiblingGroup:
         return self.suh
 
     def prime(self, x: torch.Tensor, xh: torch.Tensor):
-        """The next call with exactly this tensor uses xh (n_members, rows, k) as its rotated input."""
-        self._primed = (x, xh)
+        """The next call with this input (same tensor state) uses xh (n_members, rows, k) as its rotated input."""
+        self._primed.put(x, xh)
+
+    def serve(self, x: torch.Tensor, y: torch.Tensor):
+        """The next call with this input (same tensor state) takes its outputs from y (rows, sum(ns)), the
+        members' outputs side by side, computed ahead (fusion.py)."""
+        self._served.put(x, y)
 
     def _plan(self, rows: int, out_dtype: torch.dtype) -> TrellisGemvPlan:
         plan = self.plans.get((rows, out_dtype))
@@ -273,29 +365,48 @@ class EXL3SiblingGroup:
         return plan
 
     def gemv(self, x: torch.Tensor, out_dtype: torch.dtype) -> torch.Tensor:
-        """All members' outputs, concatenated: (rows, sum(ns)) in out_dtype (rows <= MAX_GEMV_ROWS)."""
+        """All members' outputs, concatenated: (rows, sum(ns)) in out_dtype (rows <= MAX_GEMV_ROWS). The input
+        rotations run inside the GEMV launch for fp16 input, unless a rotated input was primed."""
         rows = x.numel() // self.k
-        primed, self._primed = self._primed, None
-        xh = primed[1] if primed is not None and primed[0] is x else \
-            rot(x.reshape(rows, self.k).contiguous(), self.suh)
+        xh = self._primed.take(x)
+        if xh is None and x.dtype == torch.float16:
+            return self._plan(rows, out_dtype).rotate(x.reshape(rows, self.k).contiguous(), self.suh, self.trs)
+        if xh is None:
+            xh = rot(x.reshape(rows, self.k).contiguous(), self.suh)
         return self._plan(rows, out_dtype)(xh.contiguous(), self.trs)
 
     def gemv_rmsnorm(self, x: torch.Tensor, residual: torch.Tensor | None, weight: torch.Tensor, eps: float,
                      out_dtype: torch.dtype, residual_out: torch.Tensor | None = None,
-                     x_sumsq: torch.Tensor | None = None) -> torch.Tensor:
+                     x_sumsq: torch.Tensor | None = None, xn_out: torch.Tensor | None = None) -> torch.Tensor:
         """All members' outputs (rows, sum(ns)) for the input rmsnorm(x + residual) * weight, with the
         residual add, norm and every member's rotation inside the one GEMV launch (h = x + residual to
-        residual_out when given; x_sumsq as EXL3Linear.gemv_rmsnorm). Equal, bit for bit, to norm_rot
-        followed by gemv."""
+        residual_out, the norm's output to xn_out when given; x_sumsq as EXL3Linear.gemv_rmsnorm). Equal,
+        bit for bit, to norm_rot followed by gemv."""
         rows = x.numel() // self.k
         return self._plan(rows, out_dtype).rmsnorm(x, residual, weight, eps, self.suh, self.trs,
-                                                   residual_out=residual_out, x_sumsq=x_sumsq)
+                                                   residual_out=residual_out, x_sumsq=x_sumsq, xn_out=xn_out)
+
+    def member_output(self, x: torch.Tensor, idx: int) -> torch.Tensor:
+        """Member idx's output for input x: from the outputs of the last call with the same input state while
+        some member has not taken its own yet, else from a new call. The outputs are released once every
+        member has taken its slice."""
+        if self._outs is None or _state(x) != self._outs_state or idx in self._outs_taken:
+            outs = self(x)
+            self._outs, self._outs_state, self._outs_taken = outs, _state(x), set()
+        out = self._outs[idx]
+        self._outs_taken.add(idx)
+        if len(self._outs_taken) == len(self.members):
+            self._outs = self._outs_state = None
+            self._outs_taken = set()
+        return out
 
     def __call__(self, x: torch.Tensor) -> tuple:
-        if self._cache_x is x:
-            return self._cache_out
+        """Every member's output for input x (linear.py:172-193)."""
         in_shape, dtype = x.shape, x.dtype
         rows = x.numel() // self.k
+        y = self._served.take(x)
+        if y is not None:
+            return tuple(o.reshape(in_shape[:-1] + (n,)) for o, n in zip(torch.split(y, self.ns, dim=-1), self.ns))
         if rows > MAX_GEMV_ROWS:   # prefill: each member on its own path
             outs = []
             for m in self.members:
@@ -308,7 +419,6 @@ class EXL3SiblingGroup:
         else:
             y = self.gemv(x, dtype)
             out = tuple(o.reshape(in_shape[:-1] + (n,)) for o, n in zip(torch.split(y, self.ns, dim=-1), self.ns))
-        self._cache_x, self._cache_out = x, out
         return out
 
     def ungroup(self):
@@ -318,24 +428,27 @@ class EXL3SiblingGroup:
 
 
 class RowExactLinear(nn.Module):
-    """Dense linear whose multi-row results are bitwise those of single-row calls (linear.py:196-215):
-    rows 2..MAX_GEMV_ROWS run as independent single-row products. The EXL3 GEMV needs no such wrapper:
-    its split does not depend on the row count, so each row's result is the same for any rows."""
+    """A dense nn.Linear for speculative verify (linear.py:196-215): a BLAS library may pick another GEMM
+    kernel, and so another summation order, for 2..MAX_GEMV_ROWS rows than for one, so a verify step would
+    round differently from plain decoding. Here each of those rows is its own one-row F.linear call, so every
+    row's bits are those of a one-row call. Other row counts are a single call. The EXL3 GEMV needs no such
+    wrapper: its split depends on the shape only, so each row's result is the same for any row count."""
 
     def __init__(self, linear: nn.Linear):
         super().__init__()
+        self.in_features, self.out_features = linear.in_features, linear.out_features
         self.weight = linear.weight
         self.bias = linear.bias
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        rows = x.numel() // x.shape[-1]
-        w = self.weight.t()
-        if 1 < rows <= MAX_GEMV_ROWS:
-            x2 = x.reshape(rows, x.shape[-1])
-            y = torch.cat([x2[i:i + 1] @ w for i in range(rows)], dim=0).reshape(x.shape[:-1] + (w.shape[1],))
-        else:
-            y = x @ w
-        return y + self.bias if self.bias is not None else y
+        rows = x.numel() // self.in_features
+        if not 1 < rows <= MAX_GEMV_ROWS:
+            return F.linear(x, self.weight, self.bias)
+        flat = x.reshape(rows, self.in_features)
+        out = torch.empty((rows, self.out_features), dtype=torch.result_type(flat, self.weight), device=x.device)
+        for r in range(rows):
+            out[r:r + 1] = F.linear(flat[r:r + 1], self.weight, self.bias)
+        return out.reshape(x.shape[:-1] + (self.out_features,))
 
 
 __all__ = ["EXL3Linear", "EXL3SiblingGroup", "RowExactLinear", "unpack_signs", "had128", "EXL3_PARTS"]

@@ -26,7 +26,7 @@ import torch
 from torch import nn
 
 from .fusion import fuse_decode
-from .linear import EXL3_PARTS, EXL3Linear, EXL3SiblingGroup, _DTYPE_NAMES
+from .linear import EXL3_PARTS, EXL3Linear, EXL3SiblingGroup, RowExactLinear, _DTYPE_NAMES
 
 SIBLINGS = (("q_proj", "k_proj", "v_proj"), ("gate_proj", "up_proj"), ("in_proj_qkv", "in_proj_z"))
 
@@ -151,20 +151,38 @@ def group_siblings(model: nn.Module) -> int:
     return groups
 
 
+def row_exact_dense(model: nn.Module, prefix: str = "") -> int:
+    """Wrap every plain nn.Linear left in the model (the layers the checkpoint does not quantize) whose
+    path starts with `prefix` in RowExactLinear, so speculative-verify rows give the bits of single-row
+    decoding (loader.py:123-134). Returns how many were wrapped."""
+    wrapped = 0
+    for path, module in list(model.named_modules()):
+        if type(module) is not nn.Linear or not path.startswith(prefix):
+            continue
+        parent_path, _, name = path.rpartition(".")
+        parent = model.get_submodule(parent_path) if parent_path else model
+        setattr(parent, name, RowExactLinear(module))
+        wrapped += 1
+    return wrapped
+
+
 def load_exl3(model: nn.Module, model_path, *, sanitize_key: Callable[[str], str] = lambda k: k,
               device=None) -> dict[str, Any]:
     """Bind an EXL3 checkpoint to a torch model (the EXL3 part of loader.py:183-223): swap the linears,
-    load their tensors, group siblings and install the decode fusions (OMLX_EXL3_FUSE=0 disables them).
-    Non-EXL3 tensors of the checkpoint are the caller's to load. Returns what was done."""
+    load their tensors, group siblings, wrap the remaining dense linears for row-exact verify when
+    OMLX_EXL3_ROW_EXACT_DENSE=1 (off by default, as in the reference, loader.py:214-216), and install the
+    decode fusions (OMLX_EXL3_FUSE=0 disables them). Non-EXL3 tensors of the checkpoint are the caller's to
+    load. Returns what was done."""
     inv = inventory(model_path)
     if not inv:
         raise ValueError(f"no EXL3 trellis tensors found in {model_path}")
     swapped = swap_linears(model, inv, sanitize_key, device)
     loaded = load_exl3_tensors(model, model_path, sanitize_key)
     groups = group_siblings(model)
+    dense = row_exact_dense(model) if os.environ.get("OMLX_EXL3_ROW_EXACT_DENSE") == "1" else 0
     fused = fuse_decode(model) if os.environ.get("OMLX_EXL3_FUSE", "1") != "0" else {}
-    return {"linears": swapped, "tensors": loaded, "groups": groups, "fused": fused}
+    return {"linears": swapped, "tensors": loaded, "groups": groups, "row_exact_dense": dense, "fused": fused}
 
 
-__all__ = ["is_exl3_config", "inventory", "swap_linears", "load_exl3_tensors", "group_siblings", "load_exl3",
-           "SIBLINGS"]
+__all__ = ["is_exl3_config", "inventory", "swap_linears", "load_exl3_tensors", "group_siblings", "row_exact_dense",
+           "load_exl3", "SIBLINGS"]

@@ -10,15 +10,17 @@ device generator; suh = +-1, svh = +-1/sqrt(in_features), so that each projectio
 64 layers of random weights stay inside the fp16 range. Activations are fp16.
 
 Decode runs with a static KV cache (capacity `max_len`) and a device-side position, so one decode step
-has fixed shapes and can be captured in a HIP graph and replayed. With the decode fusions on (fuse=True,
-fused_attn=True) a decode step is five launches per layer (exl3_gemv_fused): the q/k/v GEMV with the
-RMSNorm and input rotations inside it, decode attention (exl3_attn_decode_rotate: rotary embedding, cache
-append, attention and o_proj's input rotation), the o_proj GEMV adding its output to the residual stream
-and writing the stream's 128-block sums of squares, the gate/up GEMV with its RMSNorm inside it (reading
-those sums), and the down_proj GEMV with the SwiGLU inside it and the residual add after it; the output
-head's GEMV takes the final norm the same way. Without them the residual add is fused into the RMSNorm kernel
-(exl3_rmsnorm_rotate with a residual), which writes the consumers' rotated inputs, and `fused_attn=False`
-selects the same attention as torch operations. Prefill attention uses torch operations on fp16 tensors.
+has fixed shapes and can be captured in a HIP graph and replayed. The layers are ordinary pre-norm decoder
+layers (h + attn(norm(h)), then h + mlp(norm(h))), so fusion.fuse_decode binds to them like to any
+Llama-shaped model. With fuse=True and fused_attn=True a decode step is five launches per layer
+(exl3_gemv_fused): the q/k/v GEMV with the RMSNorm and input rotations inside it, decode attention
+(exl3_attn_decode_rotate: rotary embedding, cache append, attention and o_proj's input rotation), the o_proj
+GEMV adding its output to the residual stream and writing the stream's 128-block sums of squares, the
+gate/up GEMV with its RMSNorm inside it (reading those sums), and the down_proj GEMV with the SwiGLU inside it
+and the residual add after it; the output head's GEMV takes the final norm the same way. With fuse=True and
+fused_attn=False the layers run fusion.DecodeStep around attention as torch operations; with fuse=False the
+model's own modules (torch RMSNorm, SiLU and adds, EXL3Linear calls). Prefill attention uses torch
+operations on fp16 tensors.
 """
 from __future__ import annotations
 
@@ -30,7 +32,7 @@ import torch.nn.functional as F
 from torch import nn
 
 from .fusion import fuse_decode
-from .kernels import MAX_GEMV_ROWS, attn_decode_rotate, norm_rot
+from .kernels import attn_decode_rotate
 from .linear import EXL3Linear
 from .loader import group_siblings
 
@@ -185,23 +187,10 @@ class DecoderLayer(nn.Module):
         self.post_attention_layernorm = nn.RMSNorm(cfg.hidden, eps=cfg.eps, device=device, dtype=torch.float16)
         self.mlp = MLP(cfg, gen, device)
 
-
-def add_rms_norm(norm: nn.Module, x: torch.Tensor, residual: torch.Tensor | None):
-    """h = x + residual (or x), xn = norm(h), in one kernel; when the norm was fused with its EXL3
-    consumers (fusion.fuse_decode) and rows <= MAX_GEMV_ROWS, the consumers' rotated inputs are written by
-    the same kernel and primed. Returns (xn, h)."""
-    rows = x.shape[0]
-    target = norm.__dict__.get("_exl3_target")
-    suh = target.rot_suh if (target is not None and rows <= MAX_GEMV_ROWS) else None
-    eps = norm.eps if norm.eps is not None else float(torch.finfo(x.dtype).eps)
-    if residual is None:
-        xn, xh = norm_rot(x, norm.weight, eps, suh)
-        h = x
-    else:
-        xn, xh, h = norm_rot(x, norm.weight, eps, suh, residual=residual)
-    if suh is not None:
-        target.prime(xn, xh)
-    return xn, h
+    def forward(self, h, pos, cos, sin, cos_half=None, sin_half=None):
+        """Pre-norm residual layer: h1 = h + attn(norm1(h)), h2 = h1 + mlp(norm2(h1))."""
+        h1 = h + self.self_attn(self.input_layernorm(h), pos, cos, sin, cos_half, sin_half)
+        return h1 + self.mlp(self.post_attention_layernorm(h1))
 
 
 class SyntheticDecoder(nn.Module):
@@ -270,16 +259,11 @@ class SyntheticDecoder(nn.Module):
     def forward(self, ids: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
         if self._fused_decode_ok(ids.shape[0]):
             return self._decode_fused(ids, pos)
-        x = self.model.embed_tokens(ids)                                           # (T, hidden)
-        residual = None
+        h = self.model.embed_tokens(ids)                                           # (T, hidden)
         for layer in self.model.layers:
-            xn, residual = add_rms_norm(layer.input_layernorm, x, residual)
-            x = layer.self_attn(xn, pos, self.rope_cos, self.rope_sin, self.rope_cos_half, self.rope_sin_half)
-            xn, residual = add_rms_norm(layer.post_attention_layernorm, x, residual)
-            x = layer.mlp(xn)
-        xn, _ = add_rms_norm(self.model.norm, x, residual)
-        # the head reads the primed tensor itself when T == 1 (a slice would be a new tensor)
-        return self.lm_head(xn if xn.shape[0] == 1 else xn[-1:]).float().reshape(-1)
+            h = layer(h, pos, self.rope_cos, self.rope_sin, self.rope_cos_half, self.rope_sin_half)
+        xn = self.model.norm(h)
+        return self.lm_head(xn[-1:]).float().reshape(-1)
 
 
 def _argmax(v: torch.Tensor) -> torch.Tensor:
@@ -306,4 +290,4 @@ def greedy_step(model: SyntheticDecoder, tok: torch.Tensor, pos: torch.Tensor) -
 
 greedy_step.argmax = _argmax
 
-__all__ = ["DecoderConfig", "SyntheticDecoder", "random_exl3_linear", "add_rms_norm", "greedy_step"]
+__all__ = ["DecoderConfig", "SyntheticDecoder", "random_exl3_linear", "greedy_step"]

@@ -42,3 +42,41 @@ def pytest_collection_modifyitems(config, items):
     for item in items:
         if "gpu" in item.keywords:
             item.add_marker(skip)
+
+
+class LibCalls:
+    """Counts the C-ABI kernel entry points the package calls while the context is active, by wrapping the
+    loaded library handle (queries such as exl3_last_error and exl3_gemv_workspace_bytes are not counted)."""
+
+    QUERIES = ("exl3_last_error", "exl3_gemv_workspace_bytes", "exl3_version")
+
+    def __init__(self):
+        import collections
+        self.counts = collections.Counter()
+
+    def __enter__(self):
+        from omlx_exl3_amd import _capi
+        real = _capi.lib()
+        counts = self.counts
+
+        class _Proxy:
+            def __getattr__(self, name):
+                fn = getattr(real, name)
+                if not name.startswith("exl3_") or name in LibCalls.QUERIES:
+                    return fn
+
+                def call(*args):
+                    counts[name] += 1
+                    return fn(*args)
+                return call
+
+        self._capi, self._real = _capi, real
+        _capi._lib = _Proxy()
+        return self
+
+    def __exit__(self, *exc):
+        self._capi._lib = self._real
+        return False
+
+    def total(self) -> int:
+        return sum(self.counts.values())

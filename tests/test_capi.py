@@ -85,6 +85,59 @@ def test_argument_errors(capi):
     assert lib.exl3_codebook(3, 0, p, None) == -1
 
 
+def test_overlapping_outputs_are_rejected(capi):
+    """Entry points whose workgroups read a whole row while others write reject outputs that share memory
+    with an input (host-side check, before any launch)."""
+    lib = capi.lib()
+    base = 0x100000
+    x, r, w, xn, xh, suh = (ctypes.c_void_p(base + i * 0x10000) for i in range(6))
+    rows, k = 1, 2048                 # 4 KiB per fp16 row
+    ok = lambda *a: lib.exl3_rmsnorm_rotate(*a)  # noqa: E731
+    # residual_out aliasing the residual (an in-place residual update) or x
+    assert ok(x, r, r, w, 0, 1e-6, suh, 1, rows, k, xn, xh, None) == -1 and "overlap" in _err(capi)
+    assert ok(x, r, ctypes.c_void_p(base + 0x800), w, 0, 1e-6, suh, 1, rows, k, xn, xh, None) == -1
+    # xn aliasing x, xh overlapping the residual, xn overlapping xh
+    assert ok(x, r, None, w, 0, 1e-6, suh, 1, rows, k, x, xh, None) == -1 and "overlap" in _err(capi)
+    assert ok(x, r, None, w, 0, 1e-6, suh, 1, rows, k, xn, ctypes.c_void_p(base + 0x10800), None) == -1
+    assert ok(x, None, None, w, 0, 1e-6, suh, 1, rows, k, xn, ctypes.c_void_p(base + 0x30800), None) == -1
+    # rotations: xh on top of x / gu
+    assert lib.exl3_rotate(x, 0, suh, 2, rows, k, ctypes.c_void_p(base + 0x400), None) == -1 and \
+        "overlap" in _err(capi)
+    assert lib.exl3_swiglu_rotate(x, suh, rows, k, ctypes.c_void_p(base + 0x1000), None) == -1 and \
+        "overlap" in _err(capi)
+    # the fused GEMV's norm outputs
+    trs = (ctypes.c_void_p * 3)(0x1000, 0x1000, 0x1000)
+    ns = (ctypes.c_int * 3)(128, 0, 0)
+
+    def fused(pro, xx, res, res_out, xn_out, ww, ss):
+        return lib.exl3_gemv_fused(pro, xx, res, res_out, xn_out, ww, 1e-6, ss, suh, trs, 1, ns, k, 6, 0, suh,
+                                   None, xh, 0, rows, 0, None, None, None, 0, None)
+
+    assert fused(1, x, r, r, None, w, None) == -1 and "overlap" in _err(capi)
+    assert fused(1, x, None, None, x, w, None) == -1 and "overlap" in _err(capi)
+    assert fused(1, x, r, xn, xn, w, None) == -1 and "overlap" in _err(capi)
+    # xn_out belongs to the RMSNORM prologue; ROTATE takes no norm arguments
+    assert fused(2, x, None, None, xn, None, None) == -1 and "xn_out" in _err(capi)
+    assert fused(3, x, None, None, None, w, None) == -1 and "ROTATE" in _err(capi)
+    assert fused(4, x, None, None, None, None, None) == -1 and "prologue" in _err(capi)
+
+
+def test_library_links_no_blas_library(capi):
+    """The library's dynamic dependencies: the HIP runtime and system libraries only. A build linked against
+    the system hipBLASLt / rocBLAS binds to whatever build of that library PyTorch has already loaded under
+    the same soname, and such a build faulted the GPU once; prefill GEMMs go through torch.matmul instead."""
+    import shutil
+    import subprocess
+    readelf = shutil.which("readelf")
+    if readelf is None:
+        pytest.skip("readelf not available")
+    out = subprocess.run([readelf, "-d", capi.LIB_PATH], capture_output=True, text=True, check=True).stdout
+    needed = re.findall(r"\(NEEDED\)\s+Shared library: \[([^\]]+)\]", out)
+    assert any(n.startswith("libamdhip64.so") for n in needed), needed
+    bad = [n for n in needed if any(t in n.lower() for t in ("hipblas", "rocblas", "blaslt", "tensile", "miopen"))]
+    assert not bad, bad
+
+
 def test_package_fails_loudly_without_library(tmp_path, monkeypatch):
     load_package()
     from omlx_exl3_amd import _capi

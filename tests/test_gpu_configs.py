@@ -1,0 +1,198 @@
+"""GPU parity at the benchmark's full sizes for the two largest configurations:
+
+  config 4  prefill contraction, M = 4608 rows through gate/up (5120 -> 17408) and down (17408 -> 5120) at K = 6,
+            both prefill forms (the library form with its GEMM solution table, as the benchmark times it, and
+            the fused reconstruct-in-LDS kernel), against had128(xh @ W_inner) * svh in fp32 with W_inner from
+            decode_wt (bit-exact, oracle-pinned), bar max-abs-rel 2e-3 (the GEMV/GEMM bar);
+  config 5  the 64-layer synthetic 27B-shape decoder: graph replay equals eager decoding bit for bit, the
+            five-launch decode step equals the layer-by-layer step (fusion.DecodeStep around the same
+            attention kernel) bit for bit, and prompt prefill (512 tokens) and the first decode steps agree
+            with an fp32 formulation of the same model, built layer by layer from decode_wt weights (one
+            projection reconstructed at a time), within 2% of the logit range."""
+import math
+
+import pytest
+
+from conftest import load_package
+from oracle import exl3_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+@pytest.fixture(scope="module")
+def pk():
+    return load_package()
+
+
+def _had128_t(v):
+    H = torch.tensor(O.sylvester(128), dtype=torch.float32, device=v.device) / math.sqrt(128)
+    r, n = v.shape
+    return (v.reshape(r, n // 128, 128) @ H).reshape(r, n)
+
+
+# ------------------------------------------------------------------------------------------ config 4
+@pytest.mark.parametrize("shape", ["gate_up", "down"])
+@pytest.mark.parametrize("path", ["library", "fused"])
+def test_config4_prefill_4608_rows(pk, shape, path):
+    k, n = (5120, 17408) if shape == "gate_up" else (17408, 5120)
+    K, rows = 6, 4608
+    print(f"config 4: {shape} {k}->{n} rows {rows} path {path}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(40 + len(shape))
+    tr = torch.randint(-32768, 32768, (k // 16, n // 16, 16 * K), dtype=torch.int16, device="cuda", generator=g)
+    svh = (torch.where(torch.rand(n, device="cuda", generator=g) < 0.5, -1.0, 1.0) / math.sqrt(k)).half()
+    xh = torch.randn((rows, k), device="cuda", generator=g).half()
+    y = pk.kernels.prefill_gemm(xh, tr, k, n, K, 0, svh, out_dtype=torch.float32, path=path)
+    W = pk.kernels.decode_wt(tr, k, n, K, 0).float()
+    ref = _had128_t(xh.float() @ W.T) * svh.float()
+    del W
+    err = ((y - ref).abs().max() / ref.abs().max()).item()
+    assert err < 2e-3, err
+    if path == "library":           # deterministic, and fp16 output within the bar of the fp32 output
+        y16 = pk.kernels.prefill_gemm(xh, tr, k, n, K, 0, svh, out_dtype=torch.float16, path=path)
+        assert ((y16.float() - ref).abs().max() / ref.abs().max()).item() < 2e-3
+        assert torch.equal(pk.kernels.prefill_gemm(xh, tr, k, n, K, 0, svh, out_dtype=torch.float32, path=path), y)
+
+
+# ------------------------------------------------------------------------------------------ config 5
+PROMPT = 512
+
+
+@pytest.fixture(scope="module")
+def full(pk):
+    from omlx_exl3_amd.synthetic import DecoderConfig, SyntheticDecoder
+
+    cfg = DecoderConfig(max_len=PROMPT + 64)
+    assert (cfg.n_layers, cfg.hidden, cfg.intermediate, cfg.n_heads, cfg.n_kv_heads, cfg.vocab) == \
+        (64, 5120, 17408, 48, 8, 151936)
+    print("config 5: building the 64-layer decoder", flush=True)
+    model = SyntheticDecoder(cfg, seed=2024, device="cuda")
+    ids = torch.randint(0, cfg.vocab, (PROMPT,), device="cuda", generator=torch.Generator(device="cuda").manual_seed(99))
+    logits = model(ids, torch.arange(PROMPT, device="cuda"))
+    torch.cuda.synchronize()
+    return model, ids, logits
+
+
+def _caches(model):
+    return [t for layer in model.model.layers for t in (layer.self_attn.k_cache, layer.self_attn.v_cache)]
+
+
+def _snapshot(model):
+    return [t.clone() for t in _caches(model)]
+
+
+def _restore(model, snap):
+    for t, s in zip(_caches(model), snap):
+        t.copy_(s)
+
+
+def test_config5_graph_replay_equals_eager_and_prologues_equal_layer_by_layer(pk, full):
+    from omlx_exl3_amd.synthetic import greedy_step
+
+    model, ids, logits = full
+    print("config 5: eager, layer-by-layer and graph-replayed decode steps", flush=True)
+    first = greedy_step.argmax(logits).view(1)
+    snap = _snapshot(model)
+    # eager five-launch steps
+    tok, pos = first.clone(), torch.tensor([PROMPT], device="cuda")
+    eager, toks = [], []
+    for _ in range(4):
+        greedy_step(model, tok, pos)
+        eager.append(model.last_logits.clone())
+        toks.append(tok.clone())
+    # the layer-by-layer form: DecodeStep around the same attention kernel
+    _restore(model, snap)
+    model.gemv_prologues = False
+    try:
+        tok, pos = first.clone(), torch.tensor([PROMPT], device="cuda")
+        for i in range(4):
+            greedy_step(model, tok, pos)
+            assert torch.equal(model.last_logits, eager[i]), i
+            assert torch.equal(tok, toks[i]), i
+    finally:
+        model.gemv_prologues = True
+    # one captured graph replayed
+    _restore(model, snap)
+    tok, pos = first.clone(), torch.tensor([PROMPT], device="cuda")
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        greedy_step(model, tok, pos)                    # warm-up on a side stream before capture
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        greedy_step(model, tok, pos)
+    _restore(model, snap)
+    tok.copy_(first)
+    pos.fill_(PROMPT)
+    for i in range(4):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(model.last_logits, eager[i]), i
+        assert torch.equal(tok, toks[i]) and int(pos.item()) == PROMPT + i + 1, i
+        _ = (torch.randn(4096, device="cuda") * 2).sum().item()      # unrelated eager work between replays
+    _restore(model, snap)
+
+
+def test_config5_matches_fp32_reference(pk, full):
+    """Prefill logits of the 512-token prompt and the first two greedy decode steps against an independent
+    fp32 formulation (every projection had128(had128(x * suh) @ W_inner) * svh with W_inner from decode_wt,
+    RMSNorm, rotate-half rotary embedding, causal GQA attention, SwiGLU, residuals)."""
+    from omlx_exl3_amd.synthetic import greedy_step
+
+    model, ids, logits = full
+    cfg = model.cfg
+    print("config 5: fp32 reference", flush=True)
+
+    def lin(l, x):
+        W = pk.kernels.decode_wt(l.trellis, l.in_features, l.out_features, l._K, l._cb).float()
+        y = _had128_t(_had128_t(x * l._suh.float()) @ W.t()) * l._svh.float()
+        del W
+        return y
+
+    def rms(norm, x):
+        return x * torch.rsqrt((x * x).mean(-1, keepdim=True) + cfg.eps) * norm.weight.float()
+
+    def reference(seq):
+        T, nh, nkv, hd = seq.numel(), cfg.n_heads, cfg.n_kv_heads, cfg.head_dim
+        h = model.model.embed_tokens.weight[seq].float()
+        c, s = model.rope_cos[:T].unsqueeze(1), model.rope_sin[:T].unsqueeze(1)
+        causal = torch.ones(T, T, dtype=torch.bool, device="cuda").triu(1)
+        rh = lambda x: torch.cat((-x[..., hd // 2:], x[..., :hd // 2]), dim=-1)  # noqa: E731
+        for layer in model.model.layers:
+            a = layer.self_attn
+            xn = rms(layer.input_layernorm, h)
+            q = lin(a.q_proj, xn).view(T, nh, hd)
+            k = lin(a.k_proj, xn).view(T, nkv, hd)
+            v = lin(a.v_proj, xn).view(T, nkv, hd)
+            q, k = q * c + rh(q) * s, k * c + rh(k) * s
+            k, v = k.repeat_interleave(nh // nkv, dim=1), v.repeat_interleave(nh // nkv, dim=1)
+            sc = torch.matmul(q.permute(1, 0, 2).contiguous(), k.permute(1, 2, 0).contiguous()) / math.sqrt(hd)
+            p = torch.softmax(sc.masked_fill(causal, float("-inf")), dim=-1)
+            o = torch.matmul(p, v.permute(1, 0, 2).contiguous()).permute(1, 0, 2).reshape(T, nh * hd)
+            h = h + lin(a.o_proj, o)
+            xn = rms(layer.post_attention_layernorm, h)
+            m = torch.nn.functional.silu(lin(layer.mlp.gate_proj, xn)) * lin(layer.mlp.up_proj, xn)
+            h = h + lin(layer.mlp.down_proj, m)
+        return lin(model.lm_head, rms(model.model.norm, h[-1:]))[-1]
+
+    def close(got, want):
+        rng_ = (want.max() - want.min()).item()
+        err = (got - want).abs().max().item() / rng_
+        assert err < 2e-2, err
+        top = int(torch.argmax(got))
+        assert (want.max() - want[top]).item() <= 2e-2 * rng_
+
+    snap = _snapshot(model)
+    try:
+        close(logits, reference(ids))
+        tok, pos = greedy_step.argmax(logits).view(1), torch.tensor([PROMPT], device="cuda")
+        seq = ids.clone()
+        for _ in range(2):
+            seq = torch.cat((seq, tok))
+            greedy_step(model, tok, pos)
+            close(model.last_logits, reference(seq))
+    finally:
+        _restore(model, snap)

@@ -71,7 +71,7 @@ def test_gemv_prologue_rejects_bad_arguments(pk):
     w = torch.ones(k, dtype=torch.float16, device="cuda")
     x = torch.ones(1, k, dtype=torch.float16, device="cuda")
     plan = pk.kernels.TrellisGemvPlan(k, ns, K, 0, svh, 1, torch.float16)
-    with pytest.raises(pk.kernels.Exl3Error, match="overlap"):
+    with pytest.raises((ValueError, pk.kernels.Exl3Error), match="overlap"):
         plan.rmsnorm(x, x.clone(), w, 1e-6, suh, trs, residual_out=x)
     with pytest.raises(pk.kernels.Exl3Error, match="needs a residual"):
         plan.rmsnorm(x, None, w, 1e-6, suh, trs, residual_out=torch.empty_like(x))
@@ -136,3 +136,49 @@ def test_gemv_residual_epilogue_and_block_sumsq_chain(pk, rows):
     y2 = res.clone()
     p1.fused(pk.kernels.PROLOGUE_NONE, xh, tr1, y_residual=y2, out=y2)
     assert torch.equal(y2, y)
+
+
+@pytest.mark.parametrize("k,ns,K,cb", [(5120, [1024, 256, 256], 6, 0), (2048, [2048], 4, 1), (1024, [384, 128], 3, 2)])
+def test_gemv_rmsnorm_prologue_writes_the_norm_output(pk, k, ns, K, cb):
+    """xn_out receives the norm's output, equal to exl3_rmsnorm_rotate's xn bit for bit, on both prologue
+    paths (full-row sum of squares; producer's block sums at one row), and the GEMV result is unchanged."""
+    rng = np.random.default_rng(k + 3 * K)
+    trs = _trellises(k, ns, K, 61)
+    svh = dev((rng.standard_normal(sum(ns)) / np.sqrt(k)).astype(np.float16))
+    suh = dev(np.where(rng.random((len(ns), k)) < 0.5, -1.0, 1.0).astype(np.float16))
+    w = dev((1 + 0.1 * rng.standard_normal(k)).astype(np.float16))
+    for rows in (1, 3, 16):
+        plan = pk.kernels.TrellisGemvPlan(k, ns, K, cb, svh, rows, torch.float16)
+        x = dev((3 * rng.standard_normal((rows, k))).astype(np.float16))
+        xn_ref, xh_ref = pk.kernels.norm_rot(x, w, 1e-6, suh)
+        want = plan(xh_ref, trs)
+        sums = (x.double() ** 2).reshape(rows, k // 128, 128).sum(-1).contiguous()
+        for ss in (None, sums):
+            xn = torch.full_like(x, float("nan"))
+            got = plan.rmsnorm(x, None, w, 1e-6, suh, trs, x_sumsq=ss, xn_out=xn)
+            assert torch.equal(got, want), (rows, ss is not None)
+            assert torch.equal(xn, xn_ref), (rows, ss is not None)
+        res = dev(rng.standard_normal((rows, k)).astype(np.float16))
+        xn_r, xh_r, h_r = pk.kernels.norm_rot(x, w, 1e-6, suh, residual=res)
+        xn, h = torch.empty_like(x), torch.empty_like(x)
+        got = plan.rmsnorm(x, res, w, 1e-6, suh, trs, residual_out=h, xn_out=xn)
+        assert torch.equal(got, plan(xh_r, trs)) and torch.equal(xn, xn_r) and torch.equal(h, h_r)
+
+
+@pytest.mark.parametrize("k,ns,K,cb", [(5120, [6144, 1024, 1024], 6, 0), (6144, [5120], 6, 0), (17408, [5120], 6, 0),
+                                       (1024, [256], 2, 1), (2048, [640, 128], 5, 2), (768, [128], 8, 0)])
+def test_gemv_rotate_prologue_bitwise(pk, k, ns, K, cb):
+    """The input rotation inside the GEMV launch (ROTATE prologue) gives the values of exl3_rotate followed by
+    exl3_gemv, bit for bit, for 1..3 members and rows 1..16; with the residual epilogue as well."""
+    rng = np.random.default_rng(k + len(ns) + K)
+    trs = _trellises(k, ns, K, 71)
+    svh = dev((rng.standard_normal(sum(ns)) / np.sqrt(k)).astype(np.float16))
+    suh = dev(np.where(rng.random((len(ns), k)) < 0.5, -1.0, 1.0).astype(np.float16))
+    for rows in (1, 3, 8, 16):
+        plan = pk.kernels.TrellisGemvPlan(k, ns, K, cb, svh, rows, torch.float16)
+        x = dev((2 * rng.standard_normal((rows, k))).astype(np.float16))
+        want = plan(pk.kernels.rot(x, suh), trs).clone()
+        assert torch.equal(plan.rotate(x, suh, trs), want), rows
+        res = dev(rng.standard_normal((rows, sum(ns))).astype(np.float16))
+        got = plan.rotate(x, suh, trs, y_residual=res)
+        assert torch.equal(got, (want.float() + res.float()).half()), rows

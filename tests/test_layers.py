@@ -134,6 +134,9 @@ class _Layer(nn.Module):
         self.post_attention_layernorm = nn.RMSNorm(h, dtype=torch.float16)
         self.mlp = _MLP(h, m)
 
+    def forward(self, h, **kwargs):          # the pre-norm form (never run here: no kernel runs on the CPU)
+        raise NotImplementedError
+
 
 class _Model(nn.Module):
     def __init__(self, n_layers=2, h=256, q=256, kv=128, m=384, vocab=512):
@@ -214,16 +217,19 @@ def test_load_swaps_loads_groups_and_fuses(tmp_path):
     att = m.model.layers[0].self_attn
     assert att.q_proj._group is None and att.k_proj._group is att.v_proj._group is not None
     assert isinstance(m.model.layers[0].mlp.gate_proj._group, linear.EXL3SiblingGroup)
-    assert info["fused"] == {"norm": 4, "mlp": 2, "head": 1}
-    assert type(m.model.layers[0].mlp).__name__ == "_MLP" and isinstance(m.model.layers[0].mlp, _MLP)
+    assert info["fused"] == {"layer": 2, "norm": 5, "mlp": 2, "head": 1}
+    step = m.model.layers[0].__dict__["forward"]
+    assert isinstance(step, fusion.DecodeStep) and type(m.model.layers[0]) is _Layer     # class untouched
     # values landed in the buffers
     assert torch.equal(att.k_proj.trellis, ts["model.layers.0.self_attn.k_proj.trellis"])
     down = m.model.layers[1].mlp.down_proj
     assert torch.equal(down.sv, ts["model.layers.1.mlp.down_proj.sv"]) and down.K == 6
     assert np.array_equal(down._svh.numpy(), O.unpack_signs(ts["model.layers.1.mlp.down_proj.sv"].numpy()))
-    # the norm feeding q (alone) and k/v (group) primes both consumers from one rotation input
-    tgt = m.model.layers[0].input_layernorm.__dict__["_exl3_target"]
-    assert tgt.nms == [1, 2] and tuple(tgt.rot_suh.shape) == (3, 256)
+    # the norm feeding q (alone) and k/v (group): two consumer launches, q first
+    assert step.in_consumers == [att.q_proj, att.k_proj._group] and step.out_proj is att.o_proj
+    assert step.gate_up is m.model.layers[0].mlp.gate_proj._group and step.down is m.model.layers[0].mlp.down_proj
+    assert isinstance(m.model.norm.__dict__["forward"], fusion.HeadNorm)
+    assert fusion.unfuse(m) == 3 and "forward" not in m.model.layers[0].__dict__
 
 
 def test_load_rejects_non_linear_targets_and_missing_tensors(tmp_path):
@@ -253,14 +259,26 @@ def test_fusion_eligibility():
     loader.group_siblings(m)
     m.model.layers[0].post_attention_layernorm = nn.LayerNorm(256)          # not an RMSNorm: not fused
     counts = fusion.fuse_decode(m)
-    assert counts == {"norm": 1, "mlp": 1, "head": 1}
+    assert counts == {"layer": 0, "norm": 1, "mlp": 0, "head": 1}
+
+    class GemmaRMSNorm(nn.RMSNorm):       # (1 + w) scaling in its family: never taken for a plain RMSNorm
+        pass
+
+    m2 = _Model(n_layers=1)
+    loader.swap_linears(m2, inv)
+    loader.group_siblings(m2)
+    assert fusion.fuse_decode(m2)["layer"] == 1
+    m2.model.layers[0].input_layernorm = GemmaRMSNorm(256, dtype=torch.float16)
+    assert fusion.fuse_decode(m2)["layer"] == 0
+    m2.model.layers[0].input_layernorm = nn.RMSNorm(256, dtype=torch.float32)     # fp32 weight: not fused
+    assert fusion.fuse_decode(m2)["layer"] == 0
 
 
 def test_synthetic_decoder_structure():
     cfg = synthetic.DecoderConfig(n_layers=2, hidden=256, intermediate=384, n_heads=4, n_kv_heads=2, head_dim=64,
                                   vocab=1024, max_len=32)
     model = synthetic.SyntheticDecoder(cfg, seed=1, device="cpu")
-    assert model.groups == 4 and model.fused == {"norm": 4, "mlp": 2, "head": 1}
+    assert model.groups == 4 and model.fused == {"layer": 2, "norm": 5, "mlp": 2, "head": 1}
     lin = model.model.layers[0].self_attn.q_proj
     assert lin.K == 6 and lin.codebook == 0
     assert cfg.layer_trellis_bytes() == 6 * (256 * (256 + 256) + 256 * 256 + 3 * 256 * 384) // 8
@@ -287,3 +305,68 @@ def test_prefill_gemm_table_is_well_formed():
         for k, n in [(5120, 6144), (5120, 1024), (6144, 5120), (5120, 17408), (17408, 5120)]:
             sol = entries[f"tn_{n}_{rows}_{k}_ld_{k}_{k}_{n}"]
             assert sol == "Default" or sol.split("_")[:2] in (["Gemm", "Hipblaslt"], ["Gemm", "Rocblas"])
+
+
+# ------------------------------------------------------------------------------------------ slots, row-exactness
+def test_slot_matches_only_the_same_tensor_state():
+    x = torch.randn(2, 256, dtype=torch.float16)
+    slot = linear._Slot()
+    slot.put(x, "v")
+    assert slot.take(torch.randn(2, 256, dtype=torch.float16)) is None          # another tensor
+    assert slot.take(x.view(1, 2, 256)) is None                                   # another shape
+    assert slot.take(x.view(2, 256)) == "v"                                       # a view of the same memory
+    assert slot.take(x) is None                                                   # taken once
+    slot.put(x, "w")
+    x.add_(1)                                                                     # in-place write voids it
+    assert slot.take(x) is None
+    slot.put(x, "w")
+    x[0].zero_()                                                                  # ... also through a view
+    assert slot.take(x) is None
+
+
+def test_row_exact_linear_rows_equal_single_row_calls():
+    torch.manual_seed(0)
+    dense = nn.Linear(256, 384, bias=True)
+    rel = linear.RowExactLinear(dense)
+    for rows in range(1, 11):
+        x = torch.randn(rows, 256)
+        y = rel(x)
+        want = torch.cat([dense(x[i:i + 1]) for i in range(rows)]) if rows <= 8 else dense(x)
+        assert torch.equal(y, want), rows
+    x3 = torch.randn(2, 3, 256)
+    assert torch.equal(rel(x3).reshape(6, 384), torch.cat([dense(r) for r in x3.reshape(6, 1, 256)]))
+
+
+def test_row_exact_dense_wraps_plain_linears(tmp_path, monkeypatch):
+    m = _Model(n_layers=1)
+    m.model.extra = nn.Linear(256, 128)                     # a dense layer the checkpoint does not quantize
+    ts = _checkpoint_tensors(_Model(n_layers=1), lambda p: 6)
+    _write_checkpoint(tmp_path, ts, n_files=1)
+    monkeypatch.setenv("OMLX_EXL3_ROW_EXACT_DENSE", "1")
+    info = loader.load_exl3(m, tmp_path)
+    assert info["row_exact_dense"] == 1 and isinstance(m.model.extra, linear.RowExactLinear)
+    monkeypatch.setenv("OMLX_EXL3_ROW_EXACT_DENSE", "0")
+    m2 = _Model(n_layers=1)
+    m2.model.extra = nn.Linear(256, 128)
+    assert loader.load_exl3(m2, tmp_path)["row_exact_dense"] == 0 and type(m2.model.extra) is nn.Linear
+
+
+def test_fusion_binds_transformers_llama_layers():
+    """transformers' own Llama decoder (built from a config, random init, no download) has the fusable
+    shape once its projections are EXL3Linear: every layer and the head are bound."""
+    transformers = pytest.importorskip("transformers")
+    cfg = transformers.LlamaConfig(hidden_size=256, intermediate_size=384, num_hidden_layers=2,
+                                   num_attention_heads=2, num_key_value_heads=1, head_dim=128, vocab_size=512,
+                                   max_position_embeddings=64)
+    m = transformers.LlamaForCausalLM(cfg).half()
+    inv = {p: {"trellis": ((mod.in_features // 16, mod.out_features // 16, 96), torch.int16),
+               "suh": ((mod.in_features,), torch.float16), "svh": ((mod.out_features,), torch.float16)}
+           for p, mod in m.named_modules() if isinstance(mod, nn.Linear)}
+    assert loader.swap_linears(m, inv) == 15
+    assert loader.group_siblings(m) == 4
+    assert fusion.fuse_decode(m) == {"layer": 2, "norm": 5, "mlp": 2, "head": 1}
+    step = m.model.layers[0].__dict__["forward"]
+    assert not step.tuple_out                        # transformers 5 layers return the hidden states
+    # the layer's keyword arguments reach the attention module unchanged
+    kw = step._mixer_kwargs(torch.zeros(1, 1, 256), (), {"attention_mask": None, "position_ids": 3})
+    assert kw == {"attention_mask": None, "position_ids": 3}

@@ -267,3 +267,28 @@ def test_gemv_ref_independent_formulation():
     # linearity in x
     y2 = O.gemv_ref((2 * xh.astype(np.float32)).astype(np.float16), w, svh)
     assert np.allclose(y2, 2 * y, atol=1e-9)
+
+
+def test_f32_to_bf16_matches_torch_cpu_conversion():
+    """fp32 -> bf16 round-to-nearest-even, pinned against torch's CPU conversion over random bit patterns,
+    every exact tie (both parities of the kept bit), ties +-1, the largest finite values (overflow to inf),
+    subnormals, zeros and infinities. NaNs: both give a NaN (torch writes 0xFFFF for every NaN; the oracle
+    keeps the sign and the top payload bits and sets the quiet bit, as the kernels do)."""
+    import torch
+    rng = np.random.default_rng(7)
+    pats = [rng.integers(0, 1 << 32, 200_000, dtype=np.uint64).astype(np.uint32)]
+    hi = rng.integers(0, 1 << 16, 20_000, dtype=np.uint64).astype(np.uint32) << 16
+    pats += [hi | 0x8000, hi | 0x7FFF, hi | 0x8001, hi, hi | 0xFFFF]             # ties and their neighbours
+    pats.append(np.array([0x7F7FFFFF, 0xFF7FFFFF, 0x7F7F8000, 0x7F7F7FFF, 0x00000001, 0x807FFFFF, 0x00008000,
+                          0x00018000, 0, 0x80000000, 0x7F800000, 0xFF800000], dtype=np.uint32))
+    u = np.concatenate(pats)
+    f = u.view(np.float32)
+    got = O.f32_to_bf16_bits(f)
+    want = torch.from_numpy(f.copy()).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    nan = np.isnan(f)
+    assert np.array_equal(got[~nan], want[~nan])
+    gb, wb = got[nan], want[nan]
+    assert ((gb & 0x7F80) == 0x7F80).all() and ((gb & 0x0040) != 0).all()        # quiet NaN
+    assert ((wb & 0x7F80) == 0x7F80).all() and ((wb & 0x007F) != 0).all()        # torch: a NaN too
+    assert np.array_equal(gb >> 15, (u[nan] >> 31).astype(np.uint16))            # the oracle keeps the sign
+    assert nan.sum() > 0 and (~nan).sum() > 290_000
