@@ -102,6 +102,23 @@ int exl3_gemv_ex(const uint16_t* xh, const uint32_t* const* trellis, int n_membe
                  int k, int K, int cb, const uint16_t* svh, const void* bias, void* y, int out_dtype, int rows,
                  unsigned flags, void* workspace, size_t workspace_bytes, int kt_per_split, void* stream);
 
+/* exl3_gemv without a workspace argument, for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in the reference,
+ * whose MLX runtime allocates the GEMV's partials itself (kernels.py:284-299).
+ * The split-K counters and partials live in a fixed device array of EXL3_GEMV_NOALLOC_SCRATCH_BYTES inside
+ * the library: one copy per GPU, held from the first call on that GPU until the process ends. The call
+ * allocates and frees nothing (neither here nor in any library routine it calls). A shape whose scratch need
+ * (exl3_gemv_workspace_bytes) exceeds that size is rejected with EXL3_ERR_WORKSPACE; every 27B-class
+ * projection fits at up to 8 rows. The first call on a GPU also enqueues one small fill kernel on `stream`
+ * that zeroes the counter region; every call leaves the counters at zero.
+ * All calls on one GPU share its array: calls that can overlap on that GPU (other streams, other host
+ * threads without ordering) race and give wrong results; order them on one stream.
+ * Arguments and results as exl3_gemv, bit for bit. */
+#define EXL3_GEMV_NOALLOC_SCRATCH_BYTES (8u << 20)
+int exl3_gemv_noalloc(const uint16_t* xh, const uint32_t* const* trellis, int n_members, const int* member_n,
+                      int k, int K, int cb, const uint16_t* svh, const void* bias, void* y, int out_dtype,
+                      int rows, unsigned flags, void* stream);
+
 /* exl3_gemv with the decoder's neighbouring element-wise steps inside the same launch, so the norm,
  * SwiGLU and residual-add launches around the GEMVs of a decode step disappear. No counterpart in the
  * reference, which runs norm_rot / swiglu_rot (kernels.py:408-433), the GEMV, and leaves the residual add to

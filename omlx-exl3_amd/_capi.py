@@ -27,6 +27,8 @@ _SIGNATURES = {
                            _vp, _c_size, _vp]),
     "exl3_gemv_ex": (_c_int, [_vp, _vp, _c_int, _vp, _c_int, _c_int, _c_int, _vp, _vp, _vp, _c_int, _c_int, _c_uint,
                               _vp, _c_size, _c_int, _vp]),
+    "exl3_gemv_noalloc": (_c_int, [_vp, _vp, _c_int, _vp, _c_int, _c_int, _c_int, _vp, _vp, _vp, _c_int, _c_int,
+                                   _c_uint, _vp]),
     "exl3_gemv_fused": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _vp, _c_float, _vp, _vp, _vp, _c_int, _vp, _c_int, _c_int,
                                  _c_int, _vp, _vp, _vp, _c_int, _c_int, _c_uint, _vp, _vp, _vp, _c_size, _vp]),
     "exl3_rotate": (_c_int, [_vp, _c_int, _vp, _c_int, _c_int, _c_int, _vp, _vp]),

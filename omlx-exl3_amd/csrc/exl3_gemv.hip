@@ -26,6 +26,8 @@
 // applies the 128-point Hadamard transform (stages 1, 2, ..., 64), 1/sqrt(128), svh, bias, and writes y.
 // The counter is reset by that workgroup, so it is zero again at rest. Fixed order throughout: bitwise
 // reproducible, and row r's result does not depend on the number of rows.
+#include <mutex>
+
 #include "exl3_capi_common.h"
 #include "exl3_device.h"
 #include "exl3_gemv_common.h"
@@ -825,4 +827,80 @@ extern "C" int exl3_gemv(const uint16_t* xh, const uint32_t* const* trellis, int
                          unsigned flags, void* workspace, size_t workspace_bytes, void* stream) {
   return exl3_gemv_ex(xh, trellis, n_members, member_n, k, K, cb, svh, bias, y, out_dtype, rows, flags, workspace,
                       workspace_bytes, 0, stream);
+}
+
+// ------------------------------------------------------------------------------------------------
+// exl3_gemv without a caller workspace: the split-K counters and partials live in a fixed device array of
+// the library (one copy per GPU, held until the process ends), for callers that cannot allocate.
+// ------------------------------------------------------------------------------------------------
+namespace exl3 {
+
+constexpr size_t kNoAllocScratchBytes = EXL3_GEMV_NOALLOC_SCRATCH_BYTES;
+// The counter region a call can use: blocks * 4 bytes, padded to 256; cleared on a device's first call.
+constexpr int kNoAllocClearWords = 16384;   // 64 KiB: counters of up to 2,097,152 output columns
+constexpr int kNoAllocMaxDevices = 64;
+
+// In host code this name is only a stand-in for the symbol: host code uses the per-device address that
+// hipGetSymbolAddress returns (g_scratch below), never the array itself.
+static __device__ __align__(256) uint32_t scratch[kNoAllocScratchBytes / 4];
+
+__global__ void clear_words_kernel(uint32_t* p, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
+static std::mutex g_scratch_mu;
+static void* g_scratch[kNoAllocMaxDevices];
+
+// The current device's copy of `scratch`, looked up once per device. The first call on a device also
+// enqueues a fill kernel on the caller's stream that zeroes the counter region (a kernel, not a memset, so
+// a caller capturing the stream records an ordinary kernel node); every GEMV leaves its counters at zero.
+static int noalloc_scratch(hipStream_t st, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  EXL3_REQUIRE(e == hipSuccess, EXL3_ERR_HIP, "exl3_gemv_noalloc: hipGetDevice failed: %s", hipGetErrorString(e));
+  EXL3_REQUIRE(dev >= 0 && dev < kNoAllocMaxDevices, EXL3_ERR_ARG, "exl3_gemv_noalloc: device %d beyond the %d supported",
+               dev, kNoAllocMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    EXL3_REQUIRE(e == hipSuccess && p != nullptr, EXL3_ERR_HIP,
+                 "exl3_gemv_noalloc: hipGetSymbolAddress of the scratch array failed: %s", hipGetErrorString(e));
+    clear_words_kernel<<<kNoAllocClearWords / 256, 256, 0, st>>>(static_cast<uint32_t*>(p), kNoAllocClearWords);
+    EXL3_LAUNCH_CHECK("exl3_gemv_noalloc (scratch clear)");
+    g_scratch[dev] = p;
+  }
+  *out = g_scratch[dev];
+  return EXL3_OK;
+}
+
+}  // namespace exl3
+
+extern "C" int exl3_gemv_noalloc(const uint16_t* xh, const uint32_t* const* trellis, int n_members,
+                                 const int* member_n, int k, int K, int cb, const uint16_t* svh, const void* bias,
+                                 void* y, int out_dtype, int rows, unsigned flags, void* stream) {
+  // The scratch size this call needs (either kernel), once the shape arguments are sane enough to compute it;
+  // otherwise exl3_gemv's own checks below report the bad argument.
+  if (member_n != nullptr && n_members >= 1 && n_members <= 3) {
+    long n_total = 0;
+    bool ok = true;
+    for (int i = 0; i < n_members; ++i) {
+      ok = ok && member_n[i] > 0 && member_n[i] % 128 == 0;
+      n_total += member_n[i];
+    }
+    if (ok && n_total <= (1l << 30)) {
+      const size_t need = exl3_gemv_workspace_bytes(k, (int)n_total, rows, K);
+      EXL3_REQUIRE(need <= kNoAllocScratchBytes, EXL3_ERR_WORKSPACE,
+                   "exl3_gemv_noalloc: %d x %ld at %d rows needs %zu bytes of split-K scratch, more than the "
+                   "library's fixed %zu; use exl3_gemv with a workspace",
+                   k, n_total, rows, need, kNoAllocScratchBytes);
+    }
+  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  void* ws = nullptr;
+  const int rc = noalloc_scratch(st, &ws);
+  if (rc != EXL3_OK) return rc;
+  return exl3_gemv_ex(xh, trellis, n_members, member_n, k, K, cb, svh, bias, y, out_dtype, rows, flags, ws,
+                      kNoAllocScratchBytes, 0, stream);
 }

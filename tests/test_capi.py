@@ -76,6 +76,11 @@ def test_argument_errors(capi):
     assert gemv() == -2 and "workspace" in _err(capi)
     assert lib.exl3_gemv_workspace_bytes(1024, 128, 1, 6) > 0
     assert lib.exl3_gemv_workspace_bytes(1000, 128, 1, 6) == 0
+    # the entry point without a workspace: a shape beyond its fixed scratch is refused before any HIP call
+    # (gate/up at 16 rows needs 7 splits x 16 rows x 34816 fp32 partials, more than 8 MiB)
+    ns_gu = (ctypes.c_int * 3)(17408, 17408, 0)
+    assert lib.exl3_gemv_noalloc(p, trs, 2, ns_gu, 5120, 6, 0, p, None, p, 0, 16, 0, None) == -2
+    assert "scratch" in _err(capi)
     # rotations
     assert lib.exl3_rotate(p, 0, p, 1, 1, 100, p, None) == -1 and "128" in _err(capi)
     assert lib.exl3_rotate(p, 5, p, 1, 1, 128, p, None) == -1
