@@ -50,8 +50,7 @@ extern "C" {
                                    decode half of each run through an LDS copy of the codebook's lookup table
                                    (same values, ~25% less VALU work per weight, but a table set-up and more
                                    split-K traffic per launch; slower than the default hashing kernel on the
-                                   27B decode shapes as measured). Default: every weight decoded by hashing,
-                                   one workgroup per 128-column block and k-split */
+                                   27B decode shapes as measured). Default: every weight decoded by hashing */
 
 /* Library version, (major << 16) | (minor << 8) | patch. */
 int exl3_version(void);
@@ -75,8 +74,9 @@ int exl3_reconstruct(const uint32_t* trellis, int k, int n, int K, int cb, int n
 
 /* Workspace bytes exl3_gemv needs for this shape, for either kernel (deterministic split-K partials +
  * per-block arrival counters). The workspace must be zero-filled once before its first use; every call
- * leaves the counters at zero again. One workspace must not be used by two calls in flight at the same
- * time. */
+ * leaves the counters at zero again. A workspace serves one shape (k, n_total, rows, K): to use it for
+ * another shape, zero it again first (one shape's partials may overlap another's counters). One workspace
+ * must not be used by two calls in flight at the same time. */
 size_t exl3_gemv_workspace_bytes(int k, int n_total, int rows, int K);
 
 /* Fused decode GEMV: y = had128(xh_m @ W_inner_m) * svh (+ bias) for 1..3 sibling members sharing k, K
@@ -96,7 +96,8 @@ int exl3_gemv(const uint16_t* xh, const uint32_t* const* trellis, int n_members,
 
 /* exl3_gemv with an explicit split-K granularity: kt_per_split k-tiles (16 k each, rounded up to a
  * multiple of 4) per workgroup, 0 = automatic (what exl3_gemv uses). For tuning sweeps; the workspace
- * must hold blocks*4 bytes (rounded up to 256) + S*rows*n_total*4 bytes when S = ceil((k/16)/kt_per_split) > 1.
+ * must hold blocks*256 bytes (one arrival counter per 256-byte line) + S*rows*n_total*4 bytes when
+ * S = ceil((k/16)/kt_per_split) > 1.
  * Same role as the reference's pick_tgk override (kernels.py:250-257). */
 int exl3_gemv_ex(const uint16_t* xh, const uint32_t* const* trellis, int n_members, const int* member_n,
                  int k, int K, int cb, const uint16_t* svh, const void* bias, void* y, int out_dtype, int rows,
@@ -107,9 +108,10 @@ int exl3_gemv_ex(const uint16_t* xh, const uint32_t* const* trellis, int n_membe
  * whose MLX runtime allocates the GEMV's partials itself (kernels.py:284-299).
  * The split-K counters and partials live in a fixed device array of EXL3_GEMV_NOALLOC_SCRATCH_BYTES inside
  * the library: one copy per GPU, held from the first call on that GPU until the process ends. The call
- * allocates and frees nothing (neither here nor in any library routine it calls). A shape whose scratch need
- * (exl3_gemv_workspace_bytes) exceeds that size is rejected with EXL3_ERR_WORKSPACE; every 27B-class
- * projection fits at up to 8 rows. The first call on a GPU also enqueues one small fill kernel on `stream`
+ * allocates and frees nothing (neither here nor in any library routine it calls). The counters keep a fixed
+ * 512 KiB region at the array's start (up to 262,144 output columns), so calls of different shapes follow each
+ * other safely; a shape whose partials do not fit in the rest is rejected with EXL3_ERR_WORKSPACE (every
+ * 27B-class projection fits at up to 8 rows). The first call on a GPU also enqueues one small fill kernel on `stream`
  * that zeroes the counter region; every call leaves the counters at zero.
  * All calls on one GPU share its array: calls that can overlap on that GPU (other streams, other host
  * threads without ordering) race and give wrong results; order them on one stream.

@@ -213,6 +213,63 @@ __device__ __forceinline__ uint32_t values_pos2(const uint32_t* w, uint32_t wp, 
                                                              kMask3, xor_v);
 }
 
+// ------------------------------------------------------------------------------------------------
+// 32-bit multiply form of the hash, used by the GEMV decoder. gfx950 issues v_mad_u64_u32 and v_mul_lo_u32 at
+// the rate of the 16-bit multiply-adds above, so h = s*MUL + ADD (mod 2^32) is one instruction instead of two,
+// provided the state register is clean (bits 16..31 zero): a shift, a bit-field extract or a byte permute
+// produces it, costing about what the window shift already cost.
+// ------------------------------------------------------------------------------------------------
+// Position P's 16-bit state in bits 0..15 of the result, zeros above.
+template <int K, int P>
+__device__ __forceinline__ uint32_t window_clean(const uint32_t* w, uint32_t wp) {
+  using W = Win<K, P>;
+  if constexpr (W::at_lo) {
+    return w[W::ih] & 0xFFFFu;
+  } else if constexpr (W::at_hi) {
+    return w[W::ih] >> 16;
+  } else if constexpr (W::inside) {
+    return (w[W::ih] >> W::sh) & 0xFFFFu;
+  } else {
+    const uint32_t prev = W::ih > 0 ? w[W::ih > 0 ? W::ih - 1 : 0] : wp;
+    return __builtin_amdgcn_alignbit(prev, w[W::ih], W::sh) & 0xFFFFu;
+  }
+}
+
+// h = s*MUL + ADD (mod 2^32) for a clean 16-bit state. With ADD != 0 the full 64-bit product is kept (the empty
+// asm uses its upper half), so the compiler emits one v_mad_u64_u32 instead of v_mul_lo_u32 + v_add_u32.
+template <int CB>
+__device__ __forceinline__ uint32_t hash32(uint32_t s) {
+  if constexpr (Codebook<CB>::add != 0) {
+    const uint64_t h = (uint64_t)s * Codebook<CB>::mul + Codebook<CB>::add;
+    asm volatile("" ::"v"((uint32_t)(h >> 32)));
+    return (uint32_t)h;
+  } else {
+    return s * Codebook<CB>::mul;
+  }
+}
+
+// 3INST / MCG from two hashes: fp16(a0 + b0) in the low half and fp16(a1 + b1) in the high half, where
+// (a_i, b_i) = the fp16 summand pair (h_i & mask) ^ xor (the exact decode of two positions).
+__device__ __forceinline__ uint32_t values2_h(uint32_t h0, uint32_t h1, uint32_t mask_s, uint32_t xor_v) {
+  uint32_t d, t0, t1;
+  asm("v_bitop3_b32 %[t0], %[h0], %[mask], %[xv] bitop3:0x6a\n\t"
+      "v_bitop3_b32 %[t1], %[h1], %[mask], %[xv] bitop3:0x6a\n\t"
+      "v_add_f16_sdwa %[d], %[t0], %[t0] dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1\n\t"
+      "v_add_f16_sdwa %[d], %[t1], %[t1] dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_1"
+      : [d] "=&v"(d), [t0] "=&v"(t0), [t1] "=&v"(t1)
+      : [h0] "v"(h0), [h1] "v"(h1), [mask] "s"(mask_s), [xv] "v"(xor_v));
+  return d;
+}
+
+// 3INST / MCG from two hashes: their summand pairs (the fast layout's B registers).
+__device__ __forceinline__ void summands2_h(uint32_t h0, uint32_t h1, uint32_t mask_s, uint32_t xor_v, uint32_t& u0,
+                                            uint32_t& u1) {
+  asm("v_bitop3_b32 %[u0], %[h0], %[mask], %[xv] bitop3:0x6a\n\t"
+      "v_bitop3_b32 %[u1], %[h1], %[mask], %[xv] bitop3:0x6a"
+      : [u0] "=&v"(u0), [u1] "=&v"(u1)
+      : [h0] "v"(h0), [h1] "v"(h1), [mask] "s"(mask_s), [xv] "v"(xor_v));
+}
+
 // 3INST / MCG: fp16(a0 + b0) in the low half and fp16(a1 + b1) in the high half (one RNE rounding each)
 __device__ __forceinline__ uint32_t sum_pairs(uint32_t u0, uint32_t u1) {
   uint32_t d;

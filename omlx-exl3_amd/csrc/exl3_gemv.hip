@@ -455,7 +455,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(5))) void g
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (tid == 0) {
-      const uint32_t prev = __hip_atomic_fetch_add(&a.counters[blk], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const uint32_t prev = __hip_atomic_fetch_add(&a.counters[(size_t)blk * kCounterStride], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       last = prev == (uint32_t)(a.S - 1) ? 1u : 0u;
     }
     __syncthreads();
@@ -464,7 +464,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(5))) void g
       const int r = idx >> 7, cc = idx & 127;
       bv[r][cc] = sum_splits(part + (size_t)r * a.n_total + blk * 128 + cc, pstride, a.S);
     }
-    if (tid == 0) __hip_atomic_store(&a.counters[blk], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) __hip_atomic_store(&a.counters[(size_t)blk * kCounterStride], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
   }
 
@@ -548,14 +548,18 @@ static int auto_kt_per_split(int KT, int blocks) {
 // with one.
 static int auto_k_groups(int blocks, int S) { return (long)blocks * S <= 512 ? 2 : 1; }
 
-// workspace: [per-block counters, padded to 256 B][S x rows x n_total fp32 partials]
-static size_t counters_bytes(int blocks) { return ((size_t)blocks * sizeof(uint32_t) + 255) / 256 * 256; }
+// workspace: [per-block counters, one per 256-byte line][S x rows x n_total fp32 partials]. Device-scope atomics on
+// one cache line are serialised, so packed counters made the blocks' arrivals wait on each other (measured on the
+// 27B shapes: 0.4-0.7 us per launch on q/k/v and o).
+static size_t counters_bytes(int blocks) { return (size_t)blocks * kCounterStride * sizeof(uint32_t); }
+
+static size_t partials_for(int KT, int rows, int n_total, int kps) {
+  const int S = (KT + kps - 1) / kps;
+  return S > 1 ? (size_t)S * rows * n_total * sizeof(float) : 0;
+}
 
 static size_t workspace_for(int KT, int blocks, int rows, int n_total, int kps) {
-  const int S = (KT + kps - 1) / kps;
-  size_t bytes = counters_bytes(blocks);
-  if (S > 1) bytes += (size_t)S * rows * n_total * sizeof(float);
-  return bytes;
+  return counters_bytes(blocks) + partials_for(KT, rows, n_total, kps);
 }
 
 struct GemvLaunch {
@@ -629,10 +633,13 @@ struct GemvPrologueArgs {
 };
 }  // namespace exl3
 
+// counter_region: bytes at the start of the workspace reserved for the arrival counters, 0 = exactly this shape's
+// (a workspace then serves one shape); the entry point without allocation passes a fixed region, so the counters
+// of every shape keep their place whatever the previous call's partials were.
 static int gemv_run(const uint16_t* xh, const GemvPrologueArgs& pro, const uint32_t* const* trellis, int n_members,
                     const int* member_n, int k, int K, int cb, const uint16_t* svh, const void* bias, void* y,
                     int out_dtype, int rows, unsigned flags, void* workspace, size_t workspace_bytes, int kt_per_split,
-                    void* stream) {
+                    void* stream, size_t counter_region = 0) {
   EXL3_REQUIRE((xh || pro.mode != kProNone) && trellis && member_n && svh && y, EXL3_ERR_ARG,
                "exl3_gemv: NULL pointer argument");
   EXL3_REQUIRE(n_members >= 1 && n_members <= 3, EXL3_ERR_ARG, "exl3_gemv: 1..3 members (got %d)", n_members);
@@ -664,6 +671,9 @@ static int gemv_run(const uint16_t* xh, const GemvPrologueArgs& pro, const uint3
   }
   const int KT = k / 16, blocks = n_total / 128;
   hipStream_t st = static_cast<hipStream_t>(stream);
+  const size_t creg = counter_region ? counter_region : counters_bytes(blocks);
+  EXL3_REQUIRE(creg >= counters_bytes(blocks), EXL3_ERR_ARG,
+               "exl3_gemv: %d output blocks exceed the fixed counter region of %zu bytes", blocks, creg);
   bool table_ok = pro.mode == kProNone && kt_per_split <= 0 && (flags & EXL3_GEMV_TABLE) &&
                   gemv_lut_eligible(k, K, cb, flags);
   for (int i = 0; i < n_members && table_ok; ++i) table_ok = gemv_lut_offsets_fit(k, member_n[i], K);
@@ -676,7 +686,7 @@ static int gemv_run(const uint16_t* xh, const GemvPrologueArgs& pro, const uint3
     }
     int S = 1, kps = 4;
     gemv_lut_split(KT, n_total, &S, &kps);
-    const size_t need = gemv_lut_workspace(KT, n_total, rows);
+    const size_t need = creg + gemv_lut_partials(KT, n_total, rows);
     EXL3_REQUIRE(workspace && workspace_bytes >= need && aligned(workspace, 256), EXL3_ERR_WORKSPACE,
                  "exl3_gemv: a zero-initialised, 256-byte aligned workspace of %zu bytes is needed (got %zu)", need,
                  workspace_bytes);
@@ -685,7 +695,7 @@ static int gemv_run(const uint16_t* xh, const GemvPrologueArgs& pro, const uint3
     b.bias = bias;
     b.y = y;
     b.counters = static_cast<uint32_t*>(workspace);
-    b.partials = reinterpret_cast<float*>(static_cast<char*>(workspace) + counters_bytes(blocks));
+    b.partials = reinterpret_cast<float*>(static_cast<char*>(workspace) + creg);
     b.k = k;
     b.KT = KT;
     b.rows = rows;
@@ -712,7 +722,7 @@ static int gemv_run(const uint16_t* xh, const GemvPrologueArgs& pro, const uint3
     EXL3_REQUIRE((uint64_t)(kps + 4 * WK * (kDepth + 1)) * kstride_bytes < (1ull << 32), EXL3_ERR_ARG,
                  "exl3_gemv: member %d (%d x %d) too large for 32-bit trellis offsets", i, k, member_n[i]);
   }
-  const size_t need = workspace_for(KT, blocks, rows, n_total, kps);
+  const size_t need = creg + partials_for(KT, rows, n_total, kps);
   EXL3_REQUIRE(workspace && workspace_bytes >= need && aligned(workspace, 256), EXL3_ERR_WORKSPACE,
                "exl3_gemv: a zero-initialised, 256-byte aligned workspace of %zu bytes is needed (got %zu)", need,
                workspace_bytes);
@@ -721,7 +731,7 @@ static int gemv_run(const uint16_t* xh, const GemvPrologueArgs& pro, const uint3
   a.bias = bias;
   a.y = y;
   a.counters = static_cast<uint32_t*>(workspace);
-  a.partials = reinterpret_cast<float*>(static_cast<char*>(workspace) + counters_bytes(blocks));
+  a.partials = reinterpret_cast<float*>(static_cast<char*>(workspace) + creg);
   a.k = k;
   a.KT = KT;
   a.rows = rows;
@@ -836,8 +846,11 @@ extern "C" int exl3_gemv(const uint16_t* xh, const uint32_t* const* trellis, int
 namespace exl3 {
 
 constexpr size_t kNoAllocScratchBytes = EXL3_GEMV_NOALLOC_SCRATCH_BYTES;
-// The counter region a call can use: blocks * 4 bytes, padded to 256; cleared on a device's first call.
-constexpr int kNoAllocClearWords = 16384;   // 64 KiB: counters of up to 2,097,152 output columns
+// The counters sit in a fixed region at the start of the array, one 256-byte line per 128-column block (up to
+// 2,048 blocks = 262,144 output columns), so no call's partials ever overlap another shape's counters; the region
+// is cleared on a device's first call and every call leaves it at zero.
+constexpr size_t kNoAllocCounterBytes = 512u << 10;
+constexpr int kNoAllocClearWords = (int)(kNoAllocCounterBytes / 4);
 constexpr int kNoAllocMaxDevices = 64;
 
 // In host code this name is only a stand-in for the symbol: host code uses the per-device address that
@@ -889,8 +902,11 @@ extern "C" int exl3_gemv_noalloc(const uint16_t* xh, const uint32_t* const* trel
       ok = ok && member_n[i] > 0 && member_n[i] % 128 == 0;
       n_total += member_n[i];
     }
-    if (ok && n_total <= (1l << 30)) {
-      const size_t need = exl3_gemv_workspace_bytes(k, (int)n_total, rows, K);
+    if (ok && n_total <= (1l << 30) && k > 0 && k % 16 == 0 && rows >= 1 && rows <= kMaxRows) {
+      const int KT = k / 16, blocks = (int)(n_total / 128);
+      size_t part = partials_for(KT, rows, (int)n_total, auto_kt_per_split(KT, blocks));
+      if (KT % 4 == 0) part = max(part, gemv_lut_partials(KT, (int)n_total, rows));
+      const size_t need = kNoAllocCounterBytes + part;
       EXL3_REQUIRE(need <= kNoAllocScratchBytes, EXL3_ERR_WORKSPACE,
                    "exl3_gemv_noalloc: %d x %ld at %d rows needs %zu bytes of split-K scratch, more than the "
                    "library's fixed %zu; use exl3_gemv with a workspace",
@@ -901,6 +917,8 @@ extern "C" int exl3_gemv_noalloc(const uint16_t* xh, const uint32_t* const* trel
   void* ws = nullptr;
   const int rc = noalloc_scratch(st, &ws);
   if (rc != EXL3_OK) return rc;
-  return exl3_gemv_ex(xh, trellis, n_members, member_n, k, K, cb, svh, bias, y, out_dtype, rows, flags, ws,
-                      kNoAllocScratchBytes, 0, stream);
+  const GemvPrologueArgs none{kProNone, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 0.f, nullptr, nullptr,
+                              nullptr};
+  return gemv_run(xh, none, trellis, n_members, member_n, k, K, cb, svh, bias, y, out_dtype, rows, flags, ws,
+                  kNoAllocScratchBytes, 0, stream, kNoAllocCounterBytes);
 }

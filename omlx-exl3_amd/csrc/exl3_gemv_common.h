@@ -38,27 +38,32 @@ struct GemvArgs {
 enum Prologue : int { kProNone = 0, kProNorm = 1, kProSwiglu = 2, kProRot = 3 };
 
 constexpr int kMaxRows = 16;
+constexpr int kCounterStride = 64;   // words between the split-K arrival counters of two blocks (256 bytes)
 constexpr int kBufferFlags = 0x00020000;   // raw buffer descriptor word 3 (32-bit data, no swizzle) for gfx950
 
 // Decode one run (32 positions) of K words + the word before into MFMA B registers.
 //   SPLIT: b[p] = (a_p, b_p) fp16 summands, p = 0..31
 //   pair : b[p/2] = (w_p, w_{p+1}) fp16, p even, 16 registers
+// The hash is the 32-bit multiply form (window_clean + hash32); exl3_codebook checks it against the 16-bit form
+// for every state.
 template <int K, int CB, bool SPLIT>
 __device__ __forceinline__ void decode_run(const uint32_t* w, uint32_t wp, uint32_t* b, uint32_t xor_v) {
   if constexpr (SPLIT) {
     static_for<0, 16>([&](auto P) {
       constexpr int p = 2 * decltype(P)::value;
-      summands_pos2<CB, K, p>(w, wp, xor_v, b[p], b[p + 1]);
+      summands2_h(hash32<CB>(window_clean<K, p>(w, wp)), hash32<CB>(window_clean<K, p + 1>(w, wp)), kMask3, xor_v,
+                  b[p], b[p + 1]);
     });
   } else if constexpr (CB == 2) {
     static_for<0, 16>([&](auto P) {
       constexpr int p = 2 * decltype(P)::value;
-      b[p / 2] = mul1_pair(mul1_r(hash_pos<CB, K, p>(w, wp)), mul1_r(hash_pos<CB, K, p + 1>(w, wp)));
+      b[p / 2] = mul1_pair(mul1_r(hash32<CB>(window_clean<K, p>(w, wp))), mul1_r(hash32<CB>(window_clean<K, p + 1>(w, wp))));
     });
   } else {
     static_for<0, 16>([&](auto P) {
       constexpr int p = 2 * decltype(P)::value;
-      b[p / 2] = values_pos2<CB, K, p>(w, wp, xor_v);
+      b[p / 2] = values2_h(hash32<CB>(window_clean<K, p>(w, wp)), hash32<CB>(window_clean<K, p + 1>(w, wp)), kMask3,
+                           xor_v);
     });
   }
 }
@@ -184,6 +189,7 @@ struct GemvLutArgs {
 // each a whole number of 4-k-tile steps. Depends on the shape only (row-exact results).
 void gemv_lut_split(int KT, int n_total, int* S, int* kt_per_split);
 size_t gemv_lut_workspace(int KT, int n_total, int rows);
+size_t gemv_lut_partials(int KT, int n_total, int rows);   // the partials' part of it
 bool gemv_lut_eligible(int k, int K, int cb, unsigned flags);
 bool gemv_lut_offsets_fit(int k, int n, int K);
 int gemv_lut_launch(GemvLutArgs& a, int K, int cb, int out_dtype, hipStream_t st);

@@ -208,7 +208,7 @@ __global__ __launch_bounds__(kLutThreads) void gemv_lut_kernel(GemvLutArgs a) {
   // every lane's device-scope stores are acknowledged before lane 0 counts the piece
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   uint32_t prev = 0;
-  if (lane == 0) prev = __hip_atomic_fetch_add(&a.counters[P.blk], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (lane == 0) prev = __hip_atomic_fetch_add(&a.counters[(size_t)P.blk * kCounterStride], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   prev = __builtin_amdgcn_readfirstlane(prev);
   if (prev != (uint32_t)(4 * a.S - 1)) return;
 
@@ -248,7 +248,7 @@ __global__ __launch_bounds__(kLutThreads) void gemv_lut_kernel(GemvLutArgs a) {
     store_from_f32<OT>(a.y, o, y0);
     store_from_f32<OT>(a.y, o + 1, y1);
   }
-  if (lane == 0) __hip_atomic_store(&a.counters[P.blk], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (lane == 0) __hip_atomic_store(&a.counters[(size_t)P.blk * kCounterStride], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -265,12 +265,18 @@ void gemv_lut_split(int KT, int n_total, int* S, int* kt_per_split) {
   *S = (nsteps + steps - 1) / steps;
 }
 
-static size_t lut_counters_bytes(int n_total) { return ((size_t)(n_total / 128) * sizeof(uint32_t) + 255) / 256 * 256; }
+// the same counter layout as the hashing kernel's workspace (one counter per 256-byte line), whose offset
+// exl3_gemv uses for the partials
+static size_t lut_counters_bytes(int n_total) { return (size_t)(n_total / 128) * kCounterStride * sizeof(uint32_t); }
 
-size_t gemv_lut_workspace(int KT, int n_total, int rows) {
+size_t gemv_lut_partials(int KT, int n_total, int rows) {
   int S = 1, kps = 4;
   gemv_lut_split(KT, n_total, &S, &kps);
-  return lut_counters_bytes(n_total) + (size_t)S * rows * n_total * sizeof(float);
+  return (size_t)S * rows * n_total * sizeof(float);
+}
+
+size_t gemv_lut_workspace(int KT, int n_total, int rows) {
+  return lut_counters_bytes(n_total) + gemv_lut_partials(KT, n_total, rows);
 }
 
 bool gemv_lut_eligible(int k, int K, int cb, unsigned flags) {

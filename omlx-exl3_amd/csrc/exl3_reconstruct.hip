@@ -72,10 +72,11 @@ __global__ __launch_bounds__(256) void reconstruct_kernel(const uint32_t* __rest
   }
 }
 
-// All 65,536 states through the GEMV's decode paths, with each state in either half of a register: 3INST /
-// MCG by values2 (the exact path), cross-checked against summands2 (the summand pairs of the fast path)
-// summed the same way, which writes an fp16 NaN (never a codebook value) where they disagree; MUL1 by
-// hash16 and the packed fma. The unused half of each source register holds junk bits, which the 16-bit
+// All 65,536 states through the decode paths, with each state in either half of a register: 3INST / MCG by
+// values2 (the 16-bit hash form), cross-checked against summands2 (the summand pairs of the fast layout) summed
+// the same way and against the GEMV's 32-bit multiply form (hash32 of the clean state, both layouts), which
+// write an fp16 NaN (never a codebook value) where they disagree; MUL1 by hash16 and the packed fma, checked
+// against hash32 the same way. The unused half of each source register holds junk bits, which the 16-bit
 // hash operands must ignore.
 template <int CB, bool HI>
 __global__ __launch_bounds__(256) void codebook_kernel(uint16_t* __restrict__ out) {
@@ -87,11 +88,19 @@ __global__ __launch_bounds__(256) void codebook_kernel(uint16_t* __restrict__ ou
   uint32_t d;
   if constexpr (CB == 2) {
     d = mul1_pair(mul1_r(hash16<CB, HI>(src0)), mul1_r(hash16<CB, HI>(src1)));
+    // the GEMV's 32-bit multiply form from the clean states
+    if (mul1_pair(mul1_r(hash32<CB>(s0)), mul1_r(hash32<CB>(s1))) != d) d = 0xFFFFFFFFu;
   } else {
     d = values2<CB, HI, HI>(src0, src1, kMask3, kXor3);
     uint32_t u0, u1;
     summands2<CB, HI, HI>(src0, src1, kMask3, kXor3, u0, u1);
     if (sum_pairs(u0, u1) != d) d = 0xFFFFFFFFu;
+    // the GEMV's 32-bit multiply form from the clean states, both layouts
+    const uint32_t h0 = hash32<CB>(s0), h1 = hash32<CB>(s1);
+    if (values2_h(h0, h1, kMask3, kXor3) != d) d = 0xFFFFFFFFu;
+    uint32_t v0, v1;
+    summands2_h(h0, h1, kMask3, kXor3, v0, v1);
+    if (sum_pairs(v0, v1) != d) d = 0xFFFFFFFFu;
   }
   out[s0] = (uint16_t)(d & 0xFFFFu);
   out[s1] = (uint16_t)(d >> 16);

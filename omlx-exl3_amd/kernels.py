@@ -187,8 +187,8 @@ class TrellisGemvPlan:
             KT = k // 16
             kps = (kt_per_split + 3) // 4 * 4
             S = (KT + kps - 1) // kps
-            # [block counters, padded to 256 B][S x rows x n fp32 partials]
-            nbytes = max(nbytes, (self.n // 128 * 4 + 255) // 256 * 256 + (S * rows * self.n * 4 if S > 1 else 0))
+            # [block counters, one per 256-byte line][S x rows x n fp32 partials]
+            nbytes = max(nbytes, self.n // 128 * 256 + (S * rows * self.n * 4 if S > 1 else 0))
         self.workspace = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=self.device)
         self._ns_c = (ctypes.c_int * 3)(*(list(member_ns) + [0] * (3 - len(member_ns))))
         self._tr_key = None
