@@ -405,7 +405,19 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(5))) void g
   read_A(0, X[0]);
   const int full = my_iters / D * D;
   int it = 0;
+  // Launches of two k-groups (the narrow outputs, at most 512 workgroups, all resident at once) step each
+  // wavefront's issue priority down from 3 to 0 as it completes quarters of its iterations: the SIMD's
+  // oldest-first arbitration would otherwise leave the youngest wavefronts' work for the end of the launch.
+  // Wide launches run several rounds of workgroups and are faster without it (measured).
+  const bool prio = WK > 1;
+  const int q1 = my_iters / 4, q2 = my_iters / 2, q3 = 3 * my_iters / 4;
+  if (prio) __builtin_amdgcn_s_setprio(3);
   for (; it < full; it += D) {
+    if (prio) {
+      if (it >= q3) __builtin_amdgcn_s_setprio(0);
+      else if (it >= q2) __builtin_amdgcn_s_setprio(1);
+      else if (it >= q1) __builtin_amdgcn_s_setprio(2);
+    }
     static_for<0, D>([&](auto P) {
       constexpr int d = decltype(P)::value;
       read_A(it + d + 1, X[(d + 1) & 1]);
@@ -421,6 +433,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(5))) void g
       process(st[d], X[d & 1]);
     }
   });
+
+  if (prio) __builtin_amdgcn_s_setprio(0);
 
   // ---- columns of this wavefront -> block partial (LDS), k-groups added in order 0, 1, .., WK-1 ----
   const int col_lo = (cw * 2 + (c >> 3)) * 16 + g, col_hi = col_lo + 8;
