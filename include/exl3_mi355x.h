@@ -189,6 +189,18 @@ int exl3_swiglu_rotate(const uint16_t* gu, const uint16_t* suh, int rows, int n,
 int exl3_prefill_gemm(const uint16_t* xh, const uint32_t* trellis, int k, int n, int K, int cb,
                       const uint16_t* svh, const void* bias, void* y, int out_dtype, int rows, void* stream);
 
+/* Prefill contraction on reconstructed weights: y = fp16/bf16/fp32(H128(xh @ W_inner)/sqrt(128) * svh) (+ bias)
+ * per 128-column block, by a hand-written MFMA GEMM (fp16 operands, fp32 accumulation) whose epilogue applies the
+ * output rotation. With exl3_reconstruct writing W_inner^T first, this is the reference's prefill
+ * (linear.py:97-105: decode_wt, matmul, hadamard_transform(y) * svh) with each weight decoded once and no
+ * intermediate product in HBM.
+ *   xh fp16 (rows, k), 16-byte aligned; w_t fp16 (n, k) = W_inner^T (exl3_reconstruct's output), 16-byte
+ *   aligned; svh fp16 [n]; bias NULL or [n] in out_dtype (added after the rounding to out_dtype and rounded
+ *   again, as the reference adds its bias to the output-typed product); y (rows, n) in out_dtype.
+ *   k % 64 == 0, n % 128 == 0, rows >= 1; each operand below 2 GiB. Allocates nothing; one launch. */
+int exl3_prefill_matmul(const uint16_t* xh, const uint16_t* w_t, int rows, int k, int n, const uint16_t* svh,
+                        const void* bias, void* y, int out_dtype, void* stream);
+
 /* Output rotation of the large-row prefill form, which is built as the reference's prefill is
  * (linear.py:97-105): exl3_reconstruct writes W_inner^T (bit-exact fp16), the caller multiplies
  * g = xh @ W_inner in fp16 with fp32 accumulation using its BLAS library (a plain library GEMM), and this

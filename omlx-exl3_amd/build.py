@@ -30,6 +30,13 @@ HIPCC_FLAGS = [
 ]
 
 
+# extra flags of single sources: the prefill GEMM keeps its MFMA accumulators in ordinary VGPRs (in the default
+# form the loop copies them between accumulator registers every iteration)
+FILE_FLAGS = {
+    "exl3_prefill_mm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
         if cand and os.path.exists(cand):
@@ -43,7 +50,7 @@ def sources() -> list[str]:
 
 def _compile(src: str, obj_dir: str) -> str:
     obj = os.path.join(obj_dir, os.path.basename(src)[:-4] + ".o")
-    cmd = [hipcc(), *HIPCC_FLAGS, "-c", src, "-o", obj]
+    cmd = [hipcc(), *HIPCC_FLAGS, *FILE_FLAGS.get(os.path.basename(src), []), "-c", src, "-o", obj]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src}:\n{res.stdout}\n{res.stderr}")

@@ -1,0 +1,319 @@
+// SPDX-License-Identifier: Apache-2.0
+// Prefill contraction on reconstructed weights for gfx950: y = had128(xh @ W_inner) * svh (+ bias), with
+// W_inner^T given as fp16 (n, k) as exl3_reconstruct writes it (bit-exact). Together they replace
+// EXL3Linear._prefill (reference src/omlx/exl3/linear.py:97-105: decode_wt, MLX matmul, hadamard_transform, svh)
+// with each weight decoded once per call, a hand-written MFMA GEMM, and the output rotation in its epilogue.
+//
+// Tiling: workgroup = 8 wavefronts (two per SIMD) on a BM x 256 tile of y, BM = 64 TI (TI = 4, 3 or 2, chosen per
+// shape so the tiles fill the 256 CUs in whole rounds); wavefront w owns rows 16 TI (w / 2) .. +16 TI and columns
+// 128 (w % 2) .. +128, i.e. 16 TI rows of one 128-column Hadamard block, as TI x 8 accumulator tiles of
+// v_mfma_f32_16x16x32_f16 (32 TI registers; the file is compiled with the accumulators in ordinary VGPRs, where
+// the loop keeps them in place without copies). k advances 64 per step through a double-buffered LDS tile of
+// both operands (k-contiguous rows, XOR-swizzled 16-byte pieces): the next step's global loads go straight into
+// the other LDS half (buffer loads with an LDS destination) while the current step's MFMAs run, one barrier per
+// step.
+// Epilogue (per wavefront, in registers): the 128-point FWHT of each row (stages 1, 2, 4, 8 across the 16 lanes
+// of a column group, 16, 32, 64 across the accumulator tiles), 1/sqrt(128) and svh in fp32, a rounding to the
+// output type, then the bias added in the output type (a second rounding). The reference rounds the product to
+// fp16 before its Hadamard and again after it; this path keeps fp32 through both.
+#include "exl3_capi_common.h"
+#include "exl3_device.h"
+#include "exl3_gemv_common.h"
+
+namespace exl3 {
+
+constexpr int kMmBN = 256, kMmBK = 64;
+constexpr int kMmThreads = 512, kMmWaves = kMmThreads / 64;
+// LDS tile of one operand: rows x 64 k (128 bytes = 8 16-byte pieces per row), no padding; piece p of row r sits
+// at position p ^ (r & 7). A 128-bit LDS read is served 16 lanes at a time over 64 4-byte banks (256 bytes), the
+// 16 lanes of one pass being those with equal lane bit 5 and equal parity of lane bits 2-4 (fitted to bank-
+// conflict counts of probe reads on this GPU). An MFMA fragment read takes one piece from each of 16 consecutive
+// rows (lane 16 q + c: row 16 i + c, piece 4 h + q); with this placement every pass touches 16 distinct 16-byte
+// bank groups (checked exhaustively for both fragment halves), and the loads that fill the tile write 1 KiB
+// contiguous runs, which are conflict-free too.
+__device__ __forceinline__ int mm_pos(int r, int p) { return p ^ (r & 7); }
+__device__ __forceinline__ int mm_slot(int r, int p) { return r * (kMmBK / 8) + mm_pos(r, p); }
+// instruction classes of __builtin_amdgcn_sched_group_barrier
+constexpr int kSchedMfma = 0x008, kSchedVmemRead = 0x020, kSchedDsRead = 0x100;
+
+// Issue order of a pass's MFMAs and memory instructions: one memory instruction after each MFMA while they last
+// (a memory instruction issues while the MFMA pipe works on the previous MFMA), tile loads and fragment reads
+// alternating until the loads run out.
+template <int NM, int NV, int ND>
+__device__ __forceinline__ void sched_interleave() {
+  static_assert(NV <= ND && NV + ND <= NM, "interleave pattern");
+  static_for<0, NM>([&](auto I) {
+    constexpr int m = decltype(I)::value;
+    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+    if constexpr (m < NV + ND) {
+      constexpr bool vmem = m < 2 * NV && m % 2 == 0;
+      __builtin_amdgcn_sched_group_barrier(vmem ? kSchedVmemRead : kSchedDsRead, 1, 0);
+    }
+  });
+}
+
+constexpr int kMmSlotsMax = 2 * kMmBN * (kMmBK / 8);   // A and B slots of the largest tile (TI = 4)
+
+template <int TI>
+struct MmTile {
+  static constexpr int BM = 64 * TI;                   // rows of the workgroup's tile
+  static constexpr int SA = BM * (kMmBK / 8);          // 16-byte slots of the A tile (the B tile's follow)
+  static constexpr int SB = kMmBN * (kMmBK / 8);
+  static constexpr int LA = SA / (kMmWaves * 64);      // loads per lane and step: A, B
+  static constexpr int LB = SB / (kMmWaves * 64);
+};
+
+// Workgroup b -> tile. Consecutive workgroups go to the 8 XCDs in turn, so workgroup b runs on XCD b % 8 as that
+// XCD's (b / 8)-th: tiles are numbered so each XCD works through a contiguous range of them, and inside the
+// numbering, groups of 8 tile rows are walked column by column, so the workgroups that run together on one XCD
+// share A rows and B columns in its L2. A bijection of 0 .. tiles_m tiles_n - 1.
+__device__ __forceinline__ void mm_tile_of(int b, int tiles_m, int tiles_n, int& tm, int& tn) {
+  const int T = tiles_m * tiles_n, q = T / 8, r = T % 8;
+  const int x = b % 8, local = b / 8;
+  const int t = x * q + (x < r ? x : r) + local;
+  constexpr int G = 8;
+  const int g0 = t / (G * tiles_n) * G;
+  const int gs = tiles_m - g0 < G ? tiles_m - g0 : G;   // rows in this group
+  const int u = t - g0 * tiles_n;
+  tm = g0 + u % gs;
+  tn = u / gs;
+}
+
+// One k-step of one operand tile, loaded straight from global memory into LDS (buffer loads with an LDS
+// destination: lane L of a load fills slot base + L, no registers involved). Each wavefront issues LA + LB such
+// loads per step; lane L of its j-th load of an operand fills slot (LX w + j) 64 + L of that operand's tile (LX
+// = LA or LB), i.e. row r = slot / 8 and position slot % 8, and reads the piece that position holds under the
+// swizzle. k is a multiple of 64, so a step never reads past a row; rows past the matrix read zeros through the
+// buffer descriptors.
+template <int OT, int TI>
+__global__ __launch_bounds__(kMmThreads) __attribute__((amdgpu_waves_per_eu(2))) void prefill_mm_kernel(
+    const uint16_t* __restrict__ xh, const uint16_t* __restrict__ wt, int rows, int k, int n,
+    const uint16_t* __restrict__ svh, const void* __restrict__ bias, void* __restrict__ y, int tiles_m,
+    int tiles_n) {
+  using Tl = MmTile<TI>;
+  // [stage][A slots, B slots]: 128 KiB, sized for TI = 4 whatever TI is (one workgroup per CU in every case; an
+  // LDS array whose size depends on a template parameter also makes hipcc drop the kernel's host stub when the
+  // buffer-to-LDS load builtin writes into it)
+  __shared__ u32x4 lds[2][kMmSlotsMax];
+  static_assert(Tl::SA + Tl::SB <= kMmSlotsMax, "LDS tile");
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  int tm, tn;
+  mm_tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  const int row0 = tm * Tl::BM, col0 = tn * kMmBN;
+
+  const uint32_t xbytes = (uint32_t)rows * (uint32_t)k * 2u;
+  const uint32_t wbytes = (uint32_t)n * (uint32_t)k * 2u;
+  const __amdgpu_buffer_rsrc_t rs_a = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(xh), (short)0,
+                                                                        (int)xbytes, kBufferFlags);
+  const __amdgpu_buffer_rsrc_t rs_b = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(wt), (short)0,
+                                                                        (int)wbytes, kBufferFlags);
+  // byte offsets of this lane's loads at step 0 (row (LX w + j) 8 + lane / 8 of the operand's tile, the piece at
+  // position lane % 8: the swizzle is an involution). A step adds s * 128 bytes as the loads' scalar offset,
+  // which the range check does not see, so a row past the matrix gets offset 2^31 (beyond any operand: the load
+  // returns zeros).
+  const int lr = lane >> 3, lpos = lane & 7;
+  uint32_t oa[Tl::LA], ob[Tl::LB];
+#pragma unroll
+  for (int j = 0; j < Tl::LA; ++j) {
+    const int r = (wave * Tl::LA + j) * 8 + lr;
+    const int ra = row0 + r;
+    oa[j] = ra < rows ? (uint32_t)ra * (uint32_t)k * 2u + (uint32_t)mm_pos(r, lpos) * 16u : 0x80000000u;
+  }
+#pragma unroll
+  for (int j = 0; j < Tl::LB; ++j) {
+    const int r = (wave * Tl::LB + j) * 8 + lr;
+    const int rb = col0 + r;
+    ob[j] = rb < n ? (uint32_t)rb * (uint32_t)k * 2u + (uint32_t)mm_pos(r, lpos) * 16u : 0x80000000u;
+  }
+  // (the builtin's pointer and offset arguments go through plain local variables: an argument expression that
+  // depends on a template parameter makes hipcc drop the kernel's host stub without a diagnostic)
+  auto load_stage = [&](int s, int buf) {
+    const uint32_t so = (uint32_t)s * (kMmBK * 2);
+#pragma unroll
+    for (int j = 0; j < Tl::LB; ++j) {
+      if (j < Tl::LA) {
+        u32x4* dst = &lds[buf][(wave * Tl::LA + j) * 64];
+        uint32_t vo = oa[j];
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_a, dst, 16, vo, so, 0, 0);
+      }
+      u32x4* dst = &lds[buf][Tl::SA + (wave * Tl::LB + j) * 64];
+      uint32_t vo = ob[j];
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_b, dst, 16, vo, so, 0, 0);
+    }
+  };
+
+  // MFMA operands: lane (16q + c) reads row (16 i + c) of its row band, k 8q .. 8q+7 of 32-k slice h,
+  // i.e. piece 4h + q
+  const int q = lane >> 4, c = lane & 15;
+  const int wr = (wave >> 1) * (16 * TI), wc = (wave & 1) * 128;
+  auto frag_a = [&](int buf, int r, int h) { return lds[buf][mm_slot(r, 4 * h + q)]; };
+  auto frag_b = [&](int buf, int r, int h) { return lds[buf][Tl::SA + mm_slot(r, 4 * h + q)]; };
+
+  f32x4 acc[TI][8];
+#pragma unroll
+  for (int i = 0; i < TI; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // Software pipeline over 32-k slices: the fragments of the next slice are read from LDS into one register set
+  // while the MFMAs of the current slice use the other, so every LDS read has a slice of MFMAs to land in. A pass
+  // of the loop (step s, LDS half s & 1): wait for step s + 1's tiles and barrier; then, interleaved, the tiles of
+  // step s + 2 into half s & 1, the reads of slice 0 of step s + 1 and the MFMAs of slice 1 of step s; then,
+  // interleaved, the reads of slice 1 of step s + 1 and the MFMAs of its slice 0. sched_barrier(0) keeps the
+  // compiler's scheduler from merging the phases (left alone, it sinks every LDS read below the MFMAs of the
+  // pass, and each slice then waits for its reads).
+  u32x4 fa0[TI], fb0[8], fa1[TI], fb1[8];
+  auto read_slice = [&](int buf, int h, u32x4 (&fa)[TI], u32x4 (&fb)[8]) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) fb[j] = frag_b(buf, wc + 16 * j + c, h);
+#pragma unroll
+    for (int i = 0; i < TI; ++i) fa[i] = frag_a(buf, wr + 16 * i + c, h);
+  };
+  auto mma_slice = [&](const u32x4 (&fa)[TI], const u32x4 (&fb)[8]) {
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_f16x8(fa[i]), as_f16x8(fb[j]), acc[i][j], 0, 0, 0);
+  };
+
+  const int nsteps = k / kMmBK;
+  load_stage(0, 0);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  // step 1's tiles (step 0's again when there is no step 1: a harmless reload of the idle half)
+  load_stage(nsteps > 1 ? 1 : 0, 1);
+  read_slice(0, 0, fa0, fb0);
+  read_slice(0, 1, fa1, fb1);
+  mma_slice(fa0, fb0);
+  for (int s = 0; s + 1 < nsteps; ++s) {
+    const int buf = s & 1;
+    __builtin_amdgcn_sched_barrier(0);
+    // step s + 1's tiles have landed in LDS (vmcnt) and every wavefront's reads of step s are done (the barrier
+    // waits for LDS reads) before any wavefront goes on
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    // step s + 2's tiles into the half step s used (the last pass reloads step s + 1 there, unused: the loop has
+    // no branch, which would split its body and make the compiler copy the accumulators at the join)
+    load_stage(s + 2 < nsteps ? s + 2 : s + 1, buf);
+    read_slice(buf ^ 1, 0, fa0, fb0);
+    mma_slice(fa1, fb1);
+    sched_interleave<8 * TI, Tl::LA + Tl::LB, 8 + TI>();
+    __builtin_amdgcn_sched_barrier(0);
+    read_slice(buf ^ 1, 1, fa1, fb1);
+    mma_slice(fa0, fb0);
+    sched_interleave<8 * TI, 0, 8 + TI>();
+  }
+  mma_slice(fa1, fb1);
+  // no LDS-bound load is left in flight when the workgroup ends
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  // ---------------- epilogue: FWHT over the wavefront's 128 columns, 1/sqrt(128), svh, bias ----------------
+  // acc[i][j][r] = row wr + 16 i + 4 q + r, column wc + 16 j + c of the tile
+  const int colbase = col0 + wc + c;
+  if (colbase >= n) return;
+  float sv[8], bs[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    sv[j] = f16_to_f32(svh[colbase + 16 * j]);
+    bs[j] = bias ? load_as_f32<OT>(bias, colbase + 16 * j) : 0.f;
+  }
+  // compile-time row indices (static_for) keep acc in registers whatever the unroller decides
+  static_for<0, TI>([&](auto I) {
+    constexpr int i = decltype(I)::value;
+    static_for<0, 4>([&](auto R) {
+      constexpr int r = decltype(R)::value;
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = acc[i][j][r];
+#pragma unroll
+      for (int h = 1; h < 16; h <<= 1) {
+        const bool upper = (c & h) != 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float p = __shfl_xor(v[j], h);
+          v[j] = upper ? p - v[j] : v[j] + p;
+        }
+      }
+#pragma unroll
+      for (int hj = 1; hj < 8; hj <<= 1) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          if ((j & hj) == 0) {
+            const float a = v[j], b = v[j + hj];
+            v[j] = a + b;
+            v[j + hj] = a - b;
+          }
+        }
+      }
+      const int gr = row0 + wr + 16 * i + 4 * q + r;
+      if (gr < rows) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          float o = round_through<OT>(v[j] * kHadScale * sv[j]);
+          if (bias) o = round_through<OT>(o + bs[j]);
+          store_from_f32<OT>(y, (size_t)gr * n + colbase + 16 * j, o);
+        }
+      }
+    });
+  });
+}
+
+// Rows of a tile for a shape: the tiles run one per CU in rounds of 256, so the cost of a choice is its number
+// of rounds times the work of one tile (BM rows, plus a fixed part for the prologue and epilogue).
+static int mm_pick_ti(int rows, int n) {
+  const long tiles_n = (n + kMmBN - 1) / kMmBN;
+  int best = 4;
+  long best_cost = -1;
+  for (int ti = 4; ti >= 2; --ti) {
+    const long tiles = (long)((rows + 64 * ti - 1) / (64 * ti)) * tiles_n;
+    const long cost = (tiles + 255) / 256 * (64 * ti + 64);
+    if (best_cost < 0 || cost < best_cost) {
+      best = ti;
+      best_cost = cost;
+    }
+  }
+  return best;
+}
+
+template <int OT, int TI>
+static void launch_mm_ti(const uint16_t* xh, const uint16_t* wt, int rows, int k, int n, const uint16_t* svh,
+                         const void* bias, void* y, hipStream_t st) {
+  const int tiles_m = (rows + MmTile<TI>::BM - 1) / MmTile<TI>::BM, tiles_n = (n + kMmBN - 1) / kMmBN;
+  prefill_mm_kernel<OT, TI><<<tiles_m * tiles_n, kMmThreads, 0, st>>>(xh, wt, rows, k, n, svh, bias, y, tiles_m,
+                                                                      tiles_n);
+}
+
+template <int OT>
+static void launch_mm(const uint16_t* xh, const uint16_t* wt, int rows, int k, int n, const uint16_t* svh,
+                      const void* bias, void* y, hipStream_t st) {
+  const int ti = mm_pick_ti(rows, n);
+  if (ti == 4) launch_mm_ti<OT, 4>(xh, wt, rows, k, n, svh, bias, y, st);
+  else if (ti == 3) launch_mm_ti<OT, 3>(xh, wt, rows, k, n, svh, bias, y, st);
+  else launch_mm_ti<OT, 2>(xh, wt, rows, k, n, svh, bias, y, st);
+}
+
+}  // namespace exl3
+
+using namespace exl3;
+
+extern "C" int exl3_prefill_matmul(const uint16_t* xh, const uint16_t* w_t, int rows, int k, int n,
+                                   const uint16_t* svh, const void* bias, void* y, int out_dtype, void* stream) {
+  EXL3_REQUIRE(xh && w_t && svh && y, EXL3_ERR_ARG, "exl3_prefill_matmul: NULL pointer argument");
+  EXL3_REQUIRE(k > 0 && k % kMmBK == 0, EXL3_ERR_ARG, "exl3_prefill_matmul: k must be a positive multiple of 64");
+  EXL3_REQUIRE(n > 0 && n % 128 == 0, EXL3_ERR_ARG, "exl3_prefill_matmul: n must be a positive multiple of 128");
+  EXL3_REQUIRE(rows >= 1, EXL3_ERR_ARG, "exl3_prefill_matmul: rows must be >= 1");
+  EXL3_REQUIRE(out_dtype >= 0 && out_dtype <= 2, EXL3_ERR_ARG, "exl3_prefill_matmul: bad out_dtype %d", out_dtype);
+  EXL3_REQUIRE(aligned(xh, 16) && aligned(w_t, 16), EXL3_ERR_ARG,
+               "exl3_prefill_matmul: xh and w_t must be 16-byte aligned");
+  // (operands below 2 GiB keep every byte offset in 32 bits and the tile count in an int)
+  EXL3_REQUIRE((uint64_t)rows * (uint64_t)k * 2u < (1ull << 31) && (uint64_t)n * (uint64_t)k * 2u < (1ull << 31),
+               EXL3_ERR_ARG, "exl3_prefill_matmul: an operand exceeds 2 GiB");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (out_dtype == kF16) launch_mm<kF16>(xh, w_t, rows, k, n, svh, bias, y, st);
+  else if (out_dtype == kBF16) launch_mm<kBF16>(xh, w_t, rows, k, n, svh, bias, y, st);
+  else launch_mm<kF32>(xh, w_t, rows, k, n, svh, bias, y, st);
+  EXL3_LAUNCH_CHECK("exl3_prefill_matmul");
+  return EXL3_OK;
+}
