@@ -1,8 +1,9 @@
 # SPDX-License-Identifier: Apache-2.0
 """Host-side wrappers of the HIP kernels, mirroring the reference's kernel API
 (src/omlx/exl3/kernels.py): decode_wt, rot, norm_rot, swiglu_rot, TrellisGemvPlan, MAX_GEMV_ROWS, plus
-prefill_gemm (the fused replacement of decode_wt + matmul + Hadamard on the prefill path) and codebook
-(the codebook diagnostic).
+prefill_gemm (the replacement of decode_wt + matmul + Hadamard on the prefill path: weights reconstructed
+once and a hand-written MFMA GEMM with the output rotation in its epilogue, or one fused launch for small
+grids) and codebook (the codebook diagnostic).
 
 Tensors are torch tensors on the HIP device; every call is enqueued on torch's current stream and returns
 without synchronising. Argument errors raise before anything is launched (the reference asserts,
@@ -319,27 +320,47 @@ def library_gemm(a: torch.Tensor, wt: torch.Tensor, tuned: bool = True) -> torch
         tun.tuning_enable(was_tuning)
 
 
-# Row count from which prefill_gemm's "auto" path takes the library-GEMM form (reconstruct, BLAS, exl3_prefill_out_rotate)
-# instead of the fused reconstruct-in-LDS kernel (exl3_prefill_gemm). With the GEMM solution table the library
-# form is the faster one from the smallest prefill (MAX_GEMV_ROWS + 1 rows) on: a 27B layer's seven projections
-# at 9 rows take 0.48 ms against 0.71 ms fused (measured on MI355X; only gate/up-sized outputs are ~10% faster
-# fused at 9-16 rows). The fused kernel stays selectable with path="fused".
-PREFILL_LIBRARY_ROWS = MAX_GEMV_ROWS + 1
+def prefill_matmul_fills_gpu(rows: int, n: int) -> bool:
+    """True when exl3_prefill_matmul's grid, at its smallest tile (128 rows x 256 columns), has at least one
+    tile per CU of the MI355X (256): from there on the reconstruct-then-GEMM form is the faster hand-written
+    form; below it the GEMM's grid leaves CUs idle and the fused kernel, whose grid splits k, is used."""
+    return ((rows + 127) // 128) * ((n + 255) // 256) >= 256
+
+
+def prefill_matmul(xh: torch.Tensor, wt: torch.Tensor, svh: torch.Tensor, bias: torch.Tensor | None,
+                   out: torch.Tensor) -> torch.Tensor:
+    """had128(xh @ wt^T) * svh (+ bias) into out (rows, n) by the hand-written MFMA GEMM (exl3_prefill_matmul):
+    xh (rows, k) fp16, wt (n, k) fp16 = W_inner^T as exl3_reconstruct writes it."""
+    k = xh.shape[-1]
+    rows = xh.numel() // k
+    n = wt.shape[0]
+    _require(wt.dtype == torch.float16 and tuple(wt.shape) == (n, k) and wt.is_contiguous(),
+             "prefill_matmul: wt must be contiguous fp16 (n, k)")
+    _require(k % 64 == 0, "prefill_matmul: k must be a multiple of 64")
+    _require(xh.is_contiguous(), "prefill_matmul: xh must be contiguous")
+    check(lib().exl3_prefill_matmul(ptr(xh), ptr(wt), rows, k, n, ptr(svh), ptr(bias), ptr(out),
+                                    DTYPE_CODE[out.dtype], stream_handle(xh.device)), "exl3_prefill_matmul")
+    return out
+
+
+PREFILL_PATHS = ("auto", "matmul", "fused", "library")
 
 
 def prefill_gemm(xh: torch.Tensor, trellis: torch.Tensor, k: int, n: int, K: int, cb: int, svh: torch.Tensor,
                  bias: torch.Tensor | None = None, out_dtype: torch.dtype = torch.float16,
                  out: torch.Tensor | None = None, path: str = "auto", tuned_gemm: bool = True) -> torch.Tensor:
     """had128(xh @ W_inner) * svh (+ bias) for xh (rows, k) fp16 (already rotated) (linear.py:97-105).
-    path "fused": weights reconstructed in LDS and contracted on MFMA in one launch (exl3_prefill_gemm);
-    "library": the reference's structure - W_inner^T reconstructed once (exl3_reconstruct), an fp16 GEMM with
-    fp32 accumulation by the process's BLAS library (hipBLASLt through torch.matmul), then the output rotation
-    (exl3_prefill_out_rotate); "auto": the library form from PREFILL_LIBRARY_ROWS rows. tuned_gemm: the
-    library form's GEMM runs the solution GEMM_TABLE records for its shape (library_gemm)."""
+    path "matmul": W_inner^T reconstructed once (exl3_reconstruct, bit-exact fp16), then the hand-written MFMA
+    GEMM with the output rotation in its epilogue (exl3_prefill_matmul); "fused": weights reconstructed in LDS
+    and contracted on MFMA in one launch (exl3_prefill_gemm); "auto": "matmul" when its grid fills the GPU
+    (prefill_matmul_fills_gpu), else "fused". "library" is the reference's structure with the process's BLAS
+    library for the GEMM - reconstruct, an fp16 GEMM with fp32 accumulation by hipBLASLt through torch.matmul
+    (with tuned_gemm, the solution GEMM_TABLE records for its shape), then the output rotation
+    (exl3_prefill_out_rotate) - kept as a comparison form, not taken by "auto"."""
     _dev(xh, "xh")
     rows = xh.numel() // k
     _require(xh.dtype == torch.float16 and xh.numel() == rows * k, "xh must be fp16 (rows, k)")
-    _require(path in ("auto", "fused", "library"), f"prefill_gemm: unknown path {path!r}")
+    _require(path in PREFILL_PATHS, f"prefill_gemm: unknown path {path!r}")
     _require(out_dtype in DTYPE_CODE, "prefill_gemm: out_dtype fp16, bf16 or fp32")
     trellis_words(trellis, k, n, K)
     svh = svh.to(torch.float16).reshape(-1).contiguous()
@@ -350,11 +371,16 @@ def prefill_gemm(xh: torch.Tensor, trellis: torch.Tensor, k: int, n: int, K: int
     else:
         _check_out(out, (rows, n), out_dtype)
         _require(not _overlap(out, xh), "prefill_gemm: out must not overlap xh")
-    if path == "library" or (path == "auto" and rows >= PREFILL_LIBRARY_ROWS):
+    if path == "auto":
+        path = "matmul" if k % 64 == 0 and prefill_matmul_fills_gpu(rows, n) else "fused"
+    if path in ("matmul", "library"):
         wt = torch.empty((n, k), dtype=torch.float16, device=xh.device)
         check(lib().exl3_reconstruct(ptr(trellis), k, n, K, cb, 0, n // 16, ptr(wt), stream_handle(xh.device)),
               "exl3_reconstruct")
-        g = library_gemm(xh.reshape(rows, k), wt, tuned=tuned_gemm)
+        x2 = xh.reshape(rows, k)
+        if path == "matmul":
+            return prefill_matmul(x2.contiguous(), wt, svh, bias, out)
+        g = library_gemm(x2, wt, tuned=tuned_gemm)
         check(lib().exl3_prefill_out_rotate(ptr(g), rows, n, ptr(svh), ptr(bias), ptr(out), DTYPE_CODE[out_dtype],
                                             stream_handle(xh.device)), "exl3_prefill_out_rotate")
         return out

@@ -8,11 +8,11 @@ like any layer. Forward computes  y = had128( had128(x * suh) @ W_inner ) * svh 
   rows <= MAX_GEMV_ROWS (decode, speculative verify): one GEMV launch that rotates the input (fp16 input;
       other dtypes take a rotation launch first, and a primed rotated input is used as it is), reduces,
       applies the output rotation, svh and the bias, and writes the caller's dtype (kernels.TrellisGemvPlan)
-  more rows (prefill, kernels.prefill_gemm): the input rotation, then from kernels.PREFILL_LIBRARY_ROWS
-      (every prefill row count by default) the reference's own sequence: W_inner^T reconstructed once, a
-      library fp16 GEMM, then the output rotation, svh and bias in one kernel; below it, or with
-      path="fused", one launch that reconstructs trellis tiles in LDS, contracts them on MFMA and applies
-      the output rotation, svh and bias (the fp16 weight matrix is never written to memory)
+  more rows (prefill, kernels.prefill_gemm): the input rotation, then the reference's sequence on
+      hand-written kernels: W_inner^T reconstructed once (bit-exact fp16), then an MFMA GEMM whose epilogue
+      applies the output rotation, svh and bias (exl3_prefill_matmul); when that GEMM's grid would not fill
+      the GPU (few rows), one launch that reconstructs trellis tiles in LDS, contracts them on MFMA and
+      applies the output rotation, svh and bias (the fp16 weight matrix is never written to memory)
 
 EXL3SiblingGroup runs same-input siblings (q/k/v, gate/up) as one GEMV launch over their own trellis
 buffers when they share K and codebook; each member returns its slice of the output, held until every
@@ -272,8 +272,9 @@ class EXL3Linear(nn.Module):
                                                   y_sumsq=y_sumsq)
 
     def _prefill(self, xh: torch.Tensor, out_dtype: torch.dtype, bias: torch.Tensor | None) -> torch.Tensor:
-        """had128(xh @ W_inner) * svh (+ bias) for many rows (linear.py:97-105): the reconstruct + library
-        GEMM + output rotation form from kernels.PREFILL_LIBRARY_ROWS rows, the fused launch below."""
+        """had128(xh @ W_inner) * svh (+ bias) for many rows (linear.py:97-105): reconstruct + hand-written
+        GEMM with the output rotation in its epilogue, or the fused launch when that GEMM's grid would not
+        fill the GPU (kernels.prefill_gemm, path "auto")."""
         return prefill_gemm(xh, self._tr, self.in_features, self.out_features, self._K, self._cb, self._svh,
                             bias=bias, out_dtype=out_dtype)
 

@@ -29,7 +29,8 @@ def capi():
 def test_header_declares_the_entry_points():
     fns = declared_functions()
     for name in ("exl3_gemv", "exl3_reconstruct", "exl3_rotate", "exl3_rmsnorm_rotate", "exl3_swiglu_rotate",
-                 "exl3_prefill_gemm", "exl3_gemv_workspace_bytes", "exl3_version", "exl3_last_error"):
+                 "exl3_prefill_gemm", "exl3_prefill_matmul", "exl3_gemv_workspace_bytes", "exl3_version",
+                 "exl3_last_error"):
         assert name in fns
 
 
@@ -87,6 +88,15 @@ def test_argument_errors(capi):
     assert lib.exl3_rmsnorm_rotate(p, None, None, p, 2, 1e-6, p, 1, 1, 128, p, p, None) == -1
     assert lib.exl3_swiglu_rotate(p, p, 1, 100, p, None) == -1
     assert lib.exl3_prefill_gemm(p, p, 64, 100, 6, 0, p, None, p, 0, 4, None) == -1
+    # hand-written prefill GEMM: k % 64, n % 128, rows, NULL, alignment, out dtype, 2 GiB operands
+    mm = lib.exl3_prefill_matmul
+    assert mm(p, p, 4, 96, 128, p, None, p, 0, None) == -1 and "multiple of 64" in _err(capi)
+    assert mm(p, p, 4, 64, 100, p, None, p, 0, None) == -1 and "multiple of 128" in _err(capi)
+    assert mm(p, p, 0, 64, 128, p, None, p, 0, None) == -1 and "rows" in _err(capi)
+    assert mm(None, p, 4, 64, 128, p, None, p, 0, None) == -1 and "NULL" in _err(capi)
+    assert mm(ctypes.c_void_p(0x1008), p, 4, 64, 128, p, None, p, 0, None) == -1 and "aligned" in _err(capi)
+    assert mm(p, p, 4, 64, 128, p, None, p, 3, None) == -1 and "out_dtype" in _err(capi)
+    assert mm(p, p, 1 << 20, 1024, 128, p, None, p, 0, None) == -1 and "2 GiB" in _err(capi)
     assert lib.exl3_codebook(3, 0, p, None) == -1
 
 
@@ -125,6 +135,20 @@ def test_overlapping_outputs_are_rejected(capi):
     assert fused(2, x, None, None, xn, None, None) == -1 and "xn_out" in _err(capi)
     assert fused(3, x, None, None, None, w, None) == -1 and "ROTATE" in _err(capi)
     assert fused(4, x, None, None, None, None, None) == -1 and "prologue" in _err(capi)
+
+
+def test_library_has_no_unresolved_own_symbols(capi):
+    """Every exl3 symbol the library uses is defined in it (a kernel whose host stub the compiler did not emit
+    would otherwise surface only when the library is loaded on a GPU box)."""
+    import shutil
+    import subprocess
+    nm = shutil.which("nm")
+    if nm is None:
+        pytest.skip("nm not available")
+    out = subprocess.run([nm, "-D", "--undefined-only", capi.LIB_PATH], capture_output=True, text=True,
+                         check=True).stdout
+    own = [line.split()[-1] for line in out.splitlines() if "exl3" in line]
+    assert not own, own
 
 
 def test_library_links_no_blas_library(capi):

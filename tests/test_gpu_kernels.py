@@ -269,7 +269,7 @@ def test_gemv_bias_and_split_override(pk):
 
 
 # ------------------------------------------------------------------------------------------ prefill
-@pytest.mark.parametrize("path", ["fused", "library"])
+@pytest.mark.parametrize("path", ["matmul", "fused", "library"])
 @pytest.mark.parametrize("K,cb", [(6, 0), (4, 1), (3, 2), (8, 0)])
 def test_prefill_vs_oracle(pk, K, cb, path):
     k, n, rows = 512, 384, 200
@@ -283,7 +283,8 @@ def test_prefill_vs_oracle(pk, K, cb, path):
         assert O.max_abs_rel(y.float().cpu().numpy(), ref) < bar, (dt,)
 
 
-@pytest.mark.parametrize("path,rows", [("fused", 512), ("library", 512), ("library", 1100)])
+@pytest.mark.parametrize("path,rows", [("fused", 512), ("library", 512), ("library", 1100), ("matmul", 512),
+                                       ("matmul", 1100)])
 def test_prefill_27b_shape_vs_reconstruct(pk, path, rows):
     k, n, K = 5120, 17408, 6
     g = torch.Generator(device="cuda").manual_seed(3)
@@ -298,19 +299,23 @@ def test_prefill_27b_shape_vs_reconstruct(pk, path, rows):
 
 @pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16, torch.float32])
 def test_prefill_library_path_matches_fused_with_bias(pk, dt):
-    """Both prefill forms with a bias and every output dtype, ragged row count (not a multiple of the GEMM
-    or rotation tiles): within the GEMM bar of each other; the library form is deterministic."""
+    """The three prefill forms with a bias and every output dtype, ragged row count (not a multiple of the
+    GEMM or rotation tiles): within the GEMM bar of each other; the library and matmul forms are
+    deterministic."""
     k, n, K, rows = 1024, 640, 5, 777
     rng = np.random.default_rng(21)
     tr = dev(O.random_trellis(k, n, K, 31))
     svh = dev((rng.standard_normal(n) * 0.02).astype(np.float16))
     bias = dev(rng.standard_normal(n).astype(np.float32)).to(dt)
     xh = dev(rng.standard_normal((rows, k)).astype(np.float16))
-    ys = [pk.kernels.prefill_gemm(xh, tr, k, n, K, 1, svh, bias=bias, out_dtype=dt, path=p) for p in ("fused", "library")]
+    paths = ("fused", "library", "matmul")
+    ys = [pk.kernels.prefill_gemm(xh, tr, k, n, K, 1, svh, bias=bias, out_dtype=dt, path=p) for p in paths]
     bar = 1e-2 if dt == torch.bfloat16 else 2e-3
-    assert O.max_abs_rel(ys[1].float().cpu().numpy(), ys[0].float().cpu().numpy()) < bar
-    again = pk.kernels.prefill_gemm(xh, tr, k, n, K, 1, svh, bias=bias, out_dtype=dt, path="library")
-    assert torch.equal(again, ys[1])
+    for y in ys[1:]:
+        assert O.max_abs_rel(y.float().cpu().numpy(), ys[0].float().cpu().numpy()) < bar
+    for i in (1, 2):
+        again = pk.kernels.prefill_gemm(xh, tr, k, n, K, 1, svh, bias=bias, out_dtype=dt, path=paths[i])
+        assert torch.equal(again, ys[i]), paths[i]
 
 
 def test_prefill_tuned_gemm_matches_default_and_restores_tunableop(pk):
@@ -334,6 +339,39 @@ def test_prefill_tuned_gemm_matches_default_and_restores_tunableop(pk):
     assert ((y_tab - ref).abs().max() / ref.abs().max()).item() < 2e-3
     if not F._gemm_table_loaded():
         pytest.skip("GEMM solution table not accepted by this PyTorch / ROCm build (its version lines differ)")
+
+
+@pytest.mark.parametrize("rows,n,k,ti", [(4500, 17408, 128, 4), (4608, 17536, 64, 4), (4500, 5120, 256, 3),
+                                         (4608, 5248, 192, 3), (300, 384, 1024, 2), (1, 128, 64, 2)])
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16, torch.float32])
+def test_prefill_matmul_tile_heights(pk, rows, n, k, ti, dt):
+    """exl3_prefill_matmul alone on shapes that select each tile height (256, 192, 128 rows: the choice
+    depends on rows and n only), with ragged last tiles (rows and n not multiples of the tile), one and a few
+    k-steps, a bias, and every output dtype, against the fp32 torch product of the same fp16 operands (the
+    rotation and svh applied in fp32, the bias added after the rounding to the output dtype). Deterministic."""
+    tiles_n = (n + 255) // 256
+    costs = {t: ((rows + 64 * t - 1) // (64 * t) * tiles_n + 255) // 256 * (64 * t + 64) for t in (4, 3, 2)}
+    assert min(costs, key=lambda t: (costs[t], -t)) == ti   # the shape exercises the intended tile height
+    print(f"prefill_matmul rows {rows} n {n} k {k} tile rows {64 * ti} {dt}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(rows + n + k)
+    xh = (torch.randn((rows, k), device="cuda", generator=g) * 0.5).half()
+    wt = (torch.randn((n, k), device="cuda", generator=g) / math.sqrt(k)).half()
+    svh = (torch.randn(n, device="cuda", generator=g) * 0.1).half()
+    bias = (torch.randn(n, device="cuda", generator=g) * 0.1).to(dt)
+    y = torch.empty((rows, n), dtype=dt, device="cuda")
+    pk.kernels.prefill_matmul(xh, wt, svh, bias, y)
+    ref = _had128_t(xh.float() @ wt.float().t()) * svh.float()
+    ref = ref.to(dt).float() + bias.float()
+    bar = 1e-2 if dt == torch.bfloat16 else 2e-3
+    err = ((y.float() - ref).abs().max() / ref.abs().max()).item()
+    assert err < bar, err
+    y2 = torch.empty_like(y)
+    pk.kernels.prefill_matmul(xh, wt, svh, bias, y2)
+    assert torch.equal(y, y2)
+    # without a bias: the rotated product rounded once
+    pk.kernels.prefill_matmul(xh, wt, svh, None, y2)
+    ref0 = _had128_t(xh.float() @ wt.float().t()) * svh.float()
+    assert ((y2.float() - ref0).abs().max() / ref0.abs().max()).item() < bar
 
 
 def test_prefill_out_rotate_vs_torch_and_rejects(pk):
@@ -481,7 +519,8 @@ def test_gemv_small_and_ragged_k(pk, k, ns, K):
         assert O.max_abs_rel(y.cpu().numpy(), ref) < 2e-3, (k, ns, K, rows)
 
 
-@pytest.mark.parametrize("rows,path", [(9, "fused"), (9, "library"), (9, "auto"), (63, "fused"), (64, "auto")])
+@pytest.mark.parametrize("rows,path", [(9, "fused"), (9, "library"), (9, "auto"), (63, "fused"), (64, "auto"),
+                                       (1, "matmul"), (9, "matmul"), (63, "matmul"), (129, "matmul")])
 def test_prefill_row_count_edges(pk, rows, path):
     """The smallest prefill row count through both forms and the default, and a few more row counts,
     vs the oracle."""
