@@ -33,6 +33,22 @@ constexpr int kMmThreads = 512, kMmWaves = kMmThreads / 64;
 // contiguous runs, which are conflict-free too.
 __device__ __forceinline__ int mm_pos(int r, int p) { return p ^ (r & 7); }
 __device__ __forceinline__ int mm_slot(int r, int p) { return r * (kMmBK / 8) + mm_pos(r, p); }
+// v from lane (lane ^ H) of the same 16-lane row, H = 1, 2, 4, 8, by DPP moves (VALU, no LDS round trip):
+// quad_perm [1,0,3,2] and [2,3,0,1] for 1 and 2; row_half_mirror (lane ^ 7) then quad_perm [3,2,1,0] (^ 3) for 4;
+// row_mirror (lane ^ 15) then row_half_mirror (^ 7) for 8.
+template <int H>
+__device__ __forceinline__ float row_xor(float v) {
+  // (every lane reads a lane of its own row, so bound_ctrl never applies; mov_dpp has no old-value operand to copy)
+  auto dpp = [](int x, auto ctrl) { return __builtin_amdgcn_mov_dpp(x, decltype(ctrl)::value, 0xF, 0xF, true); };
+  const int x = __builtin_bit_cast(int, v);
+  int r;
+  if constexpr (H == 1) r = dpp(x, std::integral_constant<int, 0xB1>{});
+  else if constexpr (H == 2) r = dpp(x, std::integral_constant<int, 0x4E>{});
+  else if constexpr (H == 4) r = dpp(dpp(x, std::integral_constant<int, 0x141>{}), std::integral_constant<int, 0x1B>{});
+  else r = dpp(dpp(x, std::integral_constant<int, 0x140>{}), std::integral_constant<int, 0x141>{});
+  return __builtin_bit_cast(float, r);
+}
+
 // instruction classes of __builtin_amdgcn_sched_group_barrier
 constexpr int kSchedMfma = 0x008, kSchedVmemRead = 0x020, kSchedDsRead = 0x100;
 
@@ -210,32 +226,38 @@ __global__ __launch_bounds__(kMmThreads) __attribute__((amdgpu_waves_per_eu(2)))
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   // ---------------- epilogue: FWHT over the wavefront's 128 columns, 1/sqrt(128), svh, bias ----------------
-  // acc[i][j][r] = row wr + 16 i + 4 q + r, column wc + 16 j + c of the tile
+  // acc[i][j][r] = row wr + 16 i + 4 q + r, column wc + 16 j + c of the tile. fp16 / bf16 results go through a
+  // 4 KiB LDS region per wavefront (16 rows x 128 columns, 16-byte chunk k of row R at position
+  // k ^ 2 (R >> 2 & 3): conflict-free for the 2-byte writes and the 16-byte reads), so each lane stores 16
+  // contiguous bytes. The barrier: every wavefront is done with the main loop's LDS tiles.
+  if constexpr (OT != kF32) __syncthreads();
+  if (col0 + wc >= n) return;
   const int colbase = col0 + wc + c;
-  if (colbase >= n) return;
+  const bool has_bias = bias != nullptr;
   float sv[8], bs[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     sv[j] = f16_to_f32(svh[colbase + 16 * j]);
-    bs[j] = bias ? load_as_f32<OT>(bias, colbase + 16 * j) : 0.f;
+    bs[j] = has_bias ? load_as_f32<OT>(bias, colbase + 16 * j) : 0.f;
   }
+  uint16_t* stage = reinterpret_cast<uint16_t*>(&lds[0][0]) + wave * (16 * 128);
+  auto stage_at = [](int R, int col) { return R * 128 + ((((col >> 3) ^ (2 * ((R >> 2) & 3)))) << 3) + (col & 7); };
   // compile-time row indices (static_for) keep acc in registers whatever the unroller decides
   static_for<0, TI>([&](auto I) {
     constexpr int i = decltype(I)::value;
-    static_for<0, 4>([&](auto R) {
-      constexpr int r = decltype(R)::value;
+    static_for<0, 4>([&](auto RR) {
+      constexpr int r = decltype(RR)::value;
       float v[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) v[j] = acc[i][j][r];
+      // butterfly across lanes: lane c keeps v + p (c & h clear) or p - v (c & h set), as fma(sgn, v, p), which
+      // rounds exactly as the add or subtract does (sgn * v is exact)
+      static_for<0, 4>([&](auto HB) {
+        constexpr int h = 1 << decltype(HB)::value;
+        const float sgn = (c & h) ? -1.f : 1.f;
 #pragma unroll
-      for (int h = 1; h < 16; h <<= 1) {
-        const bool upper = (c & h) != 0;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float p = __shfl_xor(v[j], h);
-          v[j] = upper ? p - v[j] : v[j] + p;
-        }
-      }
+        for (int j = 0; j < 8; ++j) v[j] = __builtin_fmaf(sgn, v[j], row_xor<h>(v[j]));
+      });
 #pragma unroll
       for (int hj = 1; hj < 8; hj <<= 1) {
 #pragma unroll
@@ -248,15 +270,33 @@ __global__ __launch_bounds__(kMmThreads) __attribute__((amdgpu_waves_per_eu(2)))
         }
       }
       const int gr = row0 + wr + 16 * i + 4 * q + r;
-      if (gr < rows) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          float o = round_through<OT>(v[j] * kHadScale * sv[j]);
-          if (bias) o = round_through<OT>(o + bs[j]);
-          store_from_f32<OT>(y, (size_t)gr * n + colbase + 16 * j, o);
+      for (int j = 0; j < 8; ++j) {
+        if constexpr (OT == kF32) {
+          const float o = v[j] * kHadScale * sv[j];
+          if (gr < rows) store_from_f32<OT>(y, (size_t)gr * n + colbase + 16 * j, has_bias ? o + bs[j] : o);
+        } else {
+          // rounded to the output type, then the bias added and rounded again (a select, no branch)
+          auto bits = [](float x) { return OT == kF16 ? f32_to_f16(x) : f32_to_bf16(x); };
+          const uint16_t bo = bits(v[j] * kHadScale * sv[j]);
+          const uint16_t bb = bits((OT == kF16 ? f16_to_f32(bo) : bf16_to_f32(bo)) + bs[j]);
+          stage[stage_at(4 * q + r, 16 * j + c)] = has_bias ? bb : bo;
         }
       }
     });
+    if constexpr (OT != kF32) {
+      // this wavefront's staging writes are done (the clobber also keeps the compiler from moving them)
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int R = 4 * t + (lane >> 4), kc = lane & 15;
+        const u32x4 w = *reinterpret_cast<const u32x4*>(stage + stage_at(R, 8 * kc));
+        const int gr = row0 + wr + 16 * i + R;
+        if (gr < rows) *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(y) + (size_t)gr * n + col0 + wc + 8 * kc) = w;
+      }
+      // the reads are done before the next row block overwrites the region
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
   });
 }
 
@@ -305,8 +345,8 @@ extern "C" int exl3_prefill_matmul(const uint16_t* xh, const uint16_t* w_t, int 
   EXL3_REQUIRE(n > 0 && n % 128 == 0, EXL3_ERR_ARG, "exl3_prefill_matmul: n must be a positive multiple of 128");
   EXL3_REQUIRE(rows >= 1, EXL3_ERR_ARG, "exl3_prefill_matmul: rows must be >= 1");
   EXL3_REQUIRE(out_dtype >= 0 && out_dtype <= 2, EXL3_ERR_ARG, "exl3_prefill_matmul: bad out_dtype %d", out_dtype);
-  EXL3_REQUIRE(aligned(xh, 16) && aligned(w_t, 16), EXL3_ERR_ARG,
-               "exl3_prefill_matmul: xh and w_t must be 16-byte aligned");
+  EXL3_REQUIRE(aligned(xh, 16) && aligned(w_t, 16) && aligned(y, 16), EXL3_ERR_ARG,
+               "exl3_prefill_matmul: xh, w_t and y must be 16-byte aligned");
   // (operands below 2 GiB keep every byte offset in 32 bits and the tile count in an int)
   EXL3_REQUIRE((uint64_t)rows * (uint64_t)k * 2u < (1ull << 31) && (uint64_t)n * (uint64_t)k * 2u < (1ull << 31),
                EXL3_ERR_ARG, "exl3_prefill_matmul: an operand exceeds 2 GiB");
