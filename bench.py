@@ -16,8 +16,8 @@ timing starts.
   roofline       the GEMV kernel: algorithmic bytes per launch / its average launch duration = GPU time
                  between HIP events recorded on the replay stream around the timed replays, divided by
                  their launches; against the 8 TB/s HBM3E peak; traffic = HBM bytes per launch from
-                 rocprofv3 FETCH_SIZE / WRITE_SIZE (profiles/), or null. per_shape: medians of single
-                 eager launches bracketed by events (they include each launch's dispatch latency)
+                 rocprofv3 FETCH_SIZE / WRITE_SIZE (profiles/), or null. per_shape: each shape's launches of
+                 all layers in one graph, replayed, events around the replays / launches (as the headline)
   cpu_baseline   the NumPy oracle (reconstruct + fp32 matmul + Hadamard + svh) on the q projection
   mixed_k        config 3: the 27B projections with K drawn per tensor from {2,3,4,5,6,8}, rows 1 / 2 / 4 / 8,
                  whole layers back to back, and per K the GB/s of that K's launches (medians of single
@@ -428,29 +428,42 @@ def main() -> int:
         run_layer(items)
     torch.cuda.synchronize()
 
-    # ---- per-launch kernel durations (HIP events on the launch stream), two eager passes ----
-    per = {name: [] for name, _, _ in LAYER}
-    evs = []
-    for i in range(2 * L):
-        for name, plan, xh, trs, out, nbytes in layers[i % L]:
-            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            s.record()
-            plan(xh, trs, out=out)
-            e.record()
-            evs.append((name, nbytes, s, e))
-    torch.cuda.synchronize()
-    for name, nbytes, s, e in evs:
-        per[name].append((nbytes, s.elapsed_time(e)))
+    # ---- per-shape launch durations: one shape's launches of all layers (different weights each) captured in
+    # one graph and replayed; HIP events on the replay stream around the timed replays, divided by the launches
+    # (the way the kernels run in a decode step: back to back, no host gaps) ----
+    cap = torch.cuda.Stream(device=dev)
     per_shape = {}
-    for name, rec in per.items():
-        nb = rec[0][0]
-        med = statistics.median(ms for _, ms in rec)
-        per_shape[name] = {"bytes": nb, "median_us": round(med * 1e3, 2), "GB_s": round(nb / med / 1e6, 1),
-                           "pct_hbm_peak": round(100 * nb / med / 1e6 / HBM_PEAK_GBS, 1)}
+    for si, (name, _k, _ns) in enumerate(LAYER):
+        cap.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(cap):
+            for items in layers:
+                _n, plan, xh, trs, out, _b = items[si]
+                plan(xh, trs, out=out)
+        torch.cuda.current_stream(dev).wait_stream(cap)
+        torch.cuda.synchronize()
+        g_shape = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g_shape):
+            for items in layers:
+                _n, plan, xh, trs, out, _b = items[si]
+                plan(xh, trs, out=out)
+        for _ in range(3):
+            g_shape.replay()
+        s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = 10
+        torch.cuda.synchronize()
+        s_ev.record()
+        for _ in range(reps):
+            g_shape.replay()
+        e_ev.record()
+        torch.cuda.synchronize()
+        us = s_ev.elapsed_time(e_ev) * 1e3 / (reps * L)
+        nb = layers[0][si][5]
+        per_shape[name] = {"bytes": nb, "us_per_launch": round(us, 2), "GB_s": round(nb / us / 1e3, 1),
+                           "pct_hbm_peak": round(100 * nb / us / 1e3 / HBM_PEAK_GBS, 1)}
+        del g_shape
 
     # ---- whole-job throughput: one step = all layers' launches captured in one graph, replayed ----
     graph = torch.cuda.CUDAGraph()
-    cap = torch.cuda.Stream(device=dev)
     cap.wait_stream(torch.cuda.current_stream(dev))
     with torch.cuda.stream(cap):
         for items in layers:           # one eager pass on the capture stream before capture
