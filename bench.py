@@ -276,7 +276,7 @@ def prefill_benchmark(pk, torch, dev, rows=4608, reps=3) -> dict:
             tot[path][0] += flop
             tot[path][1] += ms
         del tr, xh, out
-    auto = "matmul" if all(pk.kernels.prefill_matmul_fills_gpu(rows, n) for n in (17408, 5120)) else "fused"
+    auto = "matmul"   # prefill_gemm's "auto" path for these shapes (k a multiple of 64)
     tf = {p: tot[p][0] / tot[p][1] / 1e9 for p in tot}
     return {"rows": rows, "path": auto, "per_proj": per[auto], "TFLOP_s": round(tf[auto], 1),
             "peak_TFLOP_s": MFMA_F16_PEAK_TFLOPS, "mfma_frac": round(tf[auto] / MFMA_F16_PEAK_TFLOPS, 4),

@@ -196,10 +196,20 @@ int exl3_prefill_gemm(const uint16_t* xh, const uint32_t* trellis, int k, int n,
  * intermediate product in HBM.
  *   xh fp16 (rows, k), 16-byte aligned; w_t fp16 (n, k) = W_inner^T (exl3_reconstruct's output), 16-byte
  *   aligned; svh fp16 [n]; bias NULL or [n] in out_dtype (added after the rounding to out_dtype and rounded
- *   again, as the reference adds its bias to the output-typed product); y (rows, n) in out_dtype.
- *   k % 64 == 0, n % 128 == 0, rows >= 1; each operand below 2 GiB. Allocates nothing; one launch. */
+ *   again, as the reference adds its bias to the output-typed product); y (rows, n) in out_dtype, 16-byte
+ *   aligned. k % 64 == 0, n % 128 == 0, rows >= 1; each operand below 2 GiB.
+ *   When the shape's tiles would leave at least half of the GPU's CUs idle (few rows), k is split over several
+ *   workgroups per tile and a second launch adds the splits in a fixed order: that needs a 16-byte aligned
+ *   workspace of exl3_prefill_matmul_workspace_bytes(rows, k, n) bytes (0 when no split is made: the workspace
+ *   may then be NULL); EXL3_ERR_WORKSPACE when it is missing or small. Results are deterministic; the split
+ *   depends on the shape only. Allocates nothing. */
 int exl3_prefill_matmul(const uint16_t* xh, const uint16_t* w_t, int rows, int k, int n, const uint16_t* svh,
-                        const void* bias, void* y, int out_dtype, void* stream);
+                        const void* bias, void* y, int out_dtype, void* workspace, size_t workspace_bytes,
+                        void* stream);
+
+/* Workspace bytes exl3_prefill_matmul needs for a shape (0: none; also 0 for an invalid shape, which the
+ * entry point then rejects). */
+size_t exl3_prefill_matmul_workspace_bytes(int rows, int k, int n);
 
 /* Output rotation of the large-row prefill form, which is built as the reference's prefill is
  * (linear.py:97-105): exl3_reconstruct writes W_inner^T (bit-exact fp16), the caller multiplies

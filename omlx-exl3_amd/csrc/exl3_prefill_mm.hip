@@ -105,7 +105,7 @@ template <int OT, int TI>
 __global__ __launch_bounds__(kMmThreads) __attribute__((amdgpu_waves_per_eu(2))) void prefill_mm_kernel(
     const uint16_t* __restrict__ xh, const uint16_t* __restrict__ wt, int rows, int k, int n,
     const uint16_t* __restrict__ svh, const void* __restrict__ bias, void* __restrict__ y, int tiles_m,
-    int tiles_n) {
+    int tiles_n, float* __restrict__ partials, int steps_per_split) {
   using Tl = MmTile<TI>;
   // [stage][A slots, B slots]: 128 KiB, sized for TI = 4 whatever TI is (one workgroup per CU in every case; an
   // LDS array whose size depends on a template parameter also makes hipcc drop the kernel's host stub when the
@@ -144,8 +144,11 @@ __global__ __launch_bounds__(kMmThreads) __attribute__((amdgpu_waves_per_eu(2)))
   }
   // (the builtin's pointer and offset arguments go through plain local variables: an argument expression that
   // depends on a template parameter makes hipcc drop the kernel's host stub without a diagnostic)
+  // k-split of this workgroup (blockIdx.y): steps s_begin .. s_begin + nsteps - 1 of the k / 64 steps
+  const int s_begin = blockIdx.y * steps_per_split;
+  const int nsteps = min(k / kMmBK - s_begin, steps_per_split);
   auto load_stage = [&](int s, int buf) {
-    const uint32_t so = (uint32_t)s * (kMmBK * 2);
+    const uint32_t so = (uint32_t)(s_begin + s) * (kMmBK * 2);
 #pragma unroll
     for (int j = 0; j < Tl::LB; ++j) {
       if (j < Tl::LA) {
@@ -194,7 +197,6 @@ __global__ __launch_bounds__(kMmThreads) __attribute__((amdgpu_waves_per_eu(2)))
         acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_f16x8(fa[i]), as_f16x8(fb[j]), acc[i][j], 0, 0, 0);
   };
 
-  const int nsteps = k / kMmBK;
   load_stage(0, 0);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
@@ -230,6 +232,24 @@ __global__ __launch_bounds__(kMmThreads) __attribute__((amdgpu_waves_per_eu(2)))
   // 4 KiB LDS region per wavefront (16 rows x 128 columns, 16-byte chunk k of row R at position
   // k ^ 2 (R >> 2 & 3): conflict-free for the 2-byte writes and the 16-byte reads), so each lane stores 16
   // contiguous bytes. The barrier: every wavefront is done with the main loop's LDS tiles.
+  if (partials != nullptr) {
+    // k split over several workgroups: this split's raw fp32 sums, (split, row, column), for the reduction
+    // launch (exl3_prefill_matmul runs it next), which adds the splits in order and applies the epilogue below
+    if (col0 + wc >= n) return;
+    float* part = partials + (size_t)blockIdx.y * rows * n;
+    static_for<0, TI>([&](auto I) {
+      constexpr int i = decltype(I)::value;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int gr = row0 + wr + 16 * i + 4 * q + r;
+        if (gr < rows) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) part[(size_t)gr * n + col0 + wc + 16 * j + c] = acc[i][j][r];
+        }
+      }
+    });
+    return;
+  }
   if constexpr (OT != kF32) __syncthreads();
   if (col0 + wc >= n) return;
   const int colbase = col0 + wc + c;
@@ -317,29 +337,111 @@ static int mm_pick_ti(int rows, int n) {
   return best;
 }
 
+// Launch plan of a shape (from rows, k and n only): tile height, and a split of k over S workgroups per tile when
+// the tiles alone would leave at least half the 256 CUs idle. S minimises an estimate of the time: rounds x steps
+// per split x ~0.55 TI us per 64-k step of a tile, plus, for S > 1, the reduction launch (S + 1 passes over an
+// fp32 rows x n array at ~4 TB/s, and ~3 us); at least 4 steps per split, at most 16 splits, the smaller S on a
+// tie. S > 1 needs a workspace of S x rows x n fp32.
+struct MmPlan {
+  int ti, tiles_m, tiles_n, splits, steps_per_split;
+};
+
+static MmPlan mm_plan(int rows, int k, int n) {
+  MmPlan p;
+  p.ti = mm_pick_ti(rows, n);
+  p.tiles_m = (rows + 64 * p.ti - 1) / (64 * p.ti);
+  p.tiles_n = (n + kMmBN - 1) / kMmBN;
+  const int nsteps = k / kMmBK;
+  const long tiles = (long)p.tiles_m * p.tiles_n;
+  const double step_us = 0.55 * p.ti, pass_us = (double)rows * n * 4.0 / 4.0e6;
+  int best_s = 1;
+  double best_cost = (double)((tiles + 255) / 256) * nsteps * step_us;
+  if (tiles <= 128) {
+    for (int S = 2; S <= 16; ++S) {
+      const int sps = (nsteps + S - 1) / S;
+      if (sps < 4) break;
+      const double cost = (double)((tiles * S + 255) / 256) * sps * step_us + (S + 1) * pass_us + 3.0;
+      if (cost < best_cost) {
+        best_s = S;
+        best_cost = cost;
+      }
+    }
+  }
+  p.steps_per_split = (nsteps + best_s - 1) / best_s;
+  p.splits = (nsteps + p.steps_per_split - 1) / p.steps_per_split;   // no empty split
+  return p;
+}
+
+static size_t mm_workspace_bytes(const MmPlan& p, int rows, int n) {
+  return p.splits > 1 ? (size_t)p.splits * (size_t)rows * (size_t)n * sizeof(float) : 0;
+}
+
+// Reduction of a split launch: y = epilogue(sum of the S partials in split order) per (row, 128-column block),
+// 16 lanes per block, 8 consecutive columns per lane (the FWHT stage order and rounding of the GEMM epilogue).
+template <int OT>
+__global__ __launch_bounds__(256) void prefill_mm_reduce_kernel(const float* __restrict__ partials, int S, int rows,
+                                                                int n, int groups, const uint16_t* __restrict__ svh,
+                                                                const void* __restrict__ bias, void* __restrict__ y) {
+  const int grp = blockIdx.x * 16 + (threadIdx.x >> 4);
+  if (grp >= groups) return;   // whole 16-lane groups leave together: the transform's shuffles stay inside one
+  const int nb = n / 128;
+  const int r = grp / nb, b = grp - r * nb;
+  const int lane = threadIdx.x & 63;
+  const int c0 = b * 128 + 8 * (lane & 15);
+  const size_t o0 = (size_t)r * n + c0, split = (size_t)rows * n;
+  float e[8];
+  {
+    const f32x4* p = reinterpret_cast<const f32x4*>(partials + o0);
+    const f32x4 a = p[0], bb = p[1];
+    e[0] = a.x; e[1] = a.y; e[2] = a.z; e[3] = a.w; e[4] = bb.x; e[5] = bb.y; e[6] = bb.z; e[7] = bb.w;
+  }
+  for (int s = 1; s < S; ++s) {
+    const f32x4* p = reinterpret_cast<const f32x4*>(partials + s * split + o0);
+    const f32x4 a = p[0], bb = p[1];
+    e[0] += a.x; e[1] += a.y; e[2] += a.z; e[3] += a.w; e[4] += bb.x; e[5] += bb.y; e[6] += bb.z; e[7] += bb.w;
+  }
+  fwht128_lane8(e, lane);
+  float o[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    o[i] = round_through<OT>(e[i] * kHadScale * f16_to_f32(svh[c0 + i]));
+    if (bias) o[i] = round_through<OT>(o[i] + load_as_f32<OT>(bias, c0 + i));
+    store_from_f32<OT>(y, o0 + i, o[i]);
+  }
+}
+
 template <int OT, int TI>
-static void launch_mm_ti(const uint16_t* xh, const uint16_t* wt, int rows, int k, int n, const uint16_t* svh,
-                         const void* bias, void* y, hipStream_t st) {
-  const int tiles_m = (rows + MmTile<TI>::BM - 1) / MmTile<TI>::BM, tiles_n = (n + kMmBN - 1) / kMmBN;
-  prefill_mm_kernel<OT, TI><<<tiles_m * tiles_n, kMmThreads, 0, st>>>(xh, wt, rows, k, n, svh, bias, y, tiles_m,
-                                                                      tiles_n);
+static void launch_mm_ti(const MmPlan& p, const uint16_t* xh, const uint16_t* wt, int rows, int k, int n,
+                         const uint16_t* svh, const void* bias, void* y, float* partials, hipStream_t st) {
+  prefill_mm_kernel<OT, TI><<<dim3(p.tiles_m * p.tiles_n, p.splits), kMmThreads, 0, st>>>(
+      xh, wt, rows, k, n, svh, bias, y, p.tiles_m, p.tiles_n, p.splits > 1 ? partials : nullptr, p.steps_per_split);
 }
 
 template <int OT>
-static void launch_mm(const uint16_t* xh, const uint16_t* wt, int rows, int k, int n, const uint16_t* svh,
-                      const void* bias, void* y, hipStream_t st) {
-  const int ti = mm_pick_ti(rows, n);
-  if (ti == 4) launch_mm_ti<OT, 4>(xh, wt, rows, k, n, svh, bias, y, st);
-  else if (ti == 3) launch_mm_ti<OT, 3>(xh, wt, rows, k, n, svh, bias, y, st);
-  else launch_mm_ti<OT, 2>(xh, wt, rows, k, n, svh, bias, y, st);
+static void launch_mm(const MmPlan& p, const uint16_t* xh, const uint16_t* wt, int rows, int k, int n,
+                      const uint16_t* svh, const void* bias, void* y, float* partials, hipStream_t st) {
+  if (p.ti == 4) launch_mm_ti<OT, 4>(p, xh, wt, rows, k, n, svh, bias, y, partials, st);
+  else if (p.ti == 3) launch_mm_ti<OT, 3>(p, xh, wt, rows, k, n, svh, bias, y, partials, st);
+  else launch_mm_ti<OT, 2>(p, xh, wt, rows, k, n, svh, bias, y, partials, st);
+  if (p.splits > 1) {
+    const int groups = rows * (n / 128);
+    prefill_mm_reduce_kernel<OT><<<(groups + 15) / 16, 256, 0, st>>>(partials, p.splits, rows, n, groups, svh, bias,
+                                                                     y);
+  }
 }
 
 }  // namespace exl3
 
 using namespace exl3;
 
+extern "C" size_t exl3_prefill_matmul_workspace_bytes(int rows, int k, int n) {
+  if (rows < 1 || k < kMmBK || k % kMmBK != 0 || n < 128 || n % 128 != 0) return 0;
+  return mm_workspace_bytes(mm_plan(rows, k, n), rows, n);
+}
+
 extern "C" int exl3_prefill_matmul(const uint16_t* xh, const uint16_t* w_t, int rows, int k, int n,
-                                   const uint16_t* svh, const void* bias, void* y, int out_dtype, void* stream) {
+                                   const uint16_t* svh, const void* bias, void* y, int out_dtype, void* workspace,
+                                   size_t workspace_bytes, void* stream) {
   EXL3_REQUIRE(xh && w_t && svh && y, EXL3_ERR_ARG, "exl3_prefill_matmul: NULL pointer argument");
   EXL3_REQUIRE(k > 0 && k % kMmBK == 0, EXL3_ERR_ARG, "exl3_prefill_matmul: k must be a positive multiple of 64");
   EXL3_REQUIRE(n > 0 && n % 128 == 0, EXL3_ERR_ARG, "exl3_prefill_matmul: n must be a positive multiple of 128");
@@ -350,10 +452,16 @@ extern "C" int exl3_prefill_matmul(const uint16_t* xh, const uint16_t* w_t, int 
   // (operands below 2 GiB keep every byte offset in 32 bits and the tile count in an int)
   EXL3_REQUIRE((uint64_t)rows * (uint64_t)k * 2u < (1ull << 31) && (uint64_t)n * (uint64_t)k * 2u < (1ull << 31),
                EXL3_ERR_ARG, "exl3_prefill_matmul: an operand exceeds 2 GiB");
+  const MmPlan p = mm_plan(rows, k, n);
+  const size_t need = mm_workspace_bytes(p, rows, n);
+  EXL3_REQUIRE(need == 0 || (workspace && workspace_bytes >= need && aligned(workspace, 16)), EXL3_ERR_WORKSPACE,
+               "exl3_prefill_matmul: this shape splits k over %d workgroups and needs a 16-byte aligned workspace of "
+               "%zu bytes (exl3_prefill_matmul_workspace_bytes), got %zu", p.splits, need, workspace_bytes);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (out_dtype == kF16) launch_mm<kF16>(xh, w_t, rows, k, n, svh, bias, y, st);
-  else if (out_dtype == kBF16) launch_mm<kBF16>(xh, w_t, rows, k, n, svh, bias, y, st);
-  else launch_mm<kF32>(xh, w_t, rows, k, n, svh, bias, y, st);
+  float* part = static_cast<float*>(workspace);
+  if (out_dtype == kF16) launch_mm<kF16>(p, xh, w_t, rows, k, n, svh, bias, y, part, st);
+  else if (out_dtype == kBF16) launch_mm<kBF16>(p, xh, w_t, rows, k, n, svh, bias, y, part, st);
+  else launch_mm<kF32>(p, xh, w_t, rows, k, n, svh, bias, y, part, st);
   EXL3_LAUNCH_CHECK("exl3_prefill_matmul");
   return EXL3_OK;
 }

@@ -320,17 +320,12 @@ def library_gemm(a: torch.Tensor, wt: torch.Tensor, tuned: bool = True) -> torch
         tun.tuning_enable(was_tuning)
 
 
-def prefill_matmul_fills_gpu(rows: int, n: int) -> bool:
-    """True when exl3_prefill_matmul's grid, at its smallest tile (128 rows x 256 columns), has at least one
-    tile per CU of the MI355X (256): from there on the reconstruct-then-GEMM form is the faster hand-written
-    form; below it the GEMM's grid leaves CUs idle and the fused kernel, whose grid splits k, is used."""
-    return ((rows + 127) // 128) * ((n + 255) // 256) >= 256
-
-
 def prefill_matmul(xh: torch.Tensor, wt: torch.Tensor, svh: torch.Tensor, bias: torch.Tensor | None,
                    out: torch.Tensor) -> torch.Tensor:
     """had128(xh @ wt^T) * svh (+ bias) into out (rows, n) by the hand-written MFMA GEMM (exl3_prefill_matmul):
-    xh (rows, k) fp16, wt (n, k) fp16 = W_inner^T as exl3_reconstruct writes it."""
+    xh (rows, k) fp16, wt (n, k) fp16 = W_inner^T as exl3_reconstruct writes it. Shapes whose tiles would leave
+    CUs idle split k over several workgroups; their fp32 workspace is allocated here, from PyTorch's caching
+    allocator, for the call."""
     k = xh.shape[-1]
     rows = xh.numel() // k
     n = wt.shape[0]
@@ -338,8 +333,11 @@ def prefill_matmul(xh: torch.Tensor, wt: torch.Tensor, svh: torch.Tensor, bias: 
              "prefill_matmul: wt must be contiguous fp16 (n, k)")
     _require(k % 64 == 0, "prefill_matmul: k must be a multiple of 64")
     _require(xh.is_contiguous(), "prefill_matmul: xh must be contiguous")
+    nbytes = lib().exl3_prefill_matmul_workspace_bytes(rows, k, n)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=xh.device) if nbytes else None
     check(lib().exl3_prefill_matmul(ptr(xh), ptr(wt), rows, k, n, ptr(svh), ptr(bias), ptr(out),
-                                    DTYPE_CODE[out.dtype], stream_handle(xh.device)), "exl3_prefill_matmul")
+                                    DTYPE_CODE[out.dtype], ptr(ws), nbytes, stream_handle(xh.device)),
+          "exl3_prefill_matmul")
     return out
 
 
@@ -351,9 +349,9 @@ def prefill_gemm(xh: torch.Tensor, trellis: torch.Tensor, k: int, n: int, K: int
                  out: torch.Tensor | None = None, path: str = "auto", tuned_gemm: bool = True) -> torch.Tensor:
     """had128(xh @ W_inner) * svh (+ bias) for xh (rows, k) fp16 (already rotated) (linear.py:97-105).
     path "matmul": W_inner^T reconstructed once (exl3_reconstruct, bit-exact fp16), then the hand-written MFMA
-    GEMM with the output rotation in its epilogue (exl3_prefill_matmul); "fused": weights reconstructed in LDS
-    and contracted on MFMA in one launch (exl3_prefill_gemm); "auto": "matmul" when its grid fills the GPU
-    (prefill_matmul_fills_gpu), else "fused". "library" is the reference's structure with the process's BLAS
+    GEMM with the output rotation in its epilogue (exl3_prefill_matmul, k split over workgroups for few rows);
+    "fused": weights reconstructed in LDS and contracted on MFMA in one launch (exl3_prefill_gemm); "auto":
+    "matmul" (k a multiple of 64, as every EXL3 layer's is), else "fused". "library" is the reference's structure with the process's BLAS
     library for the GEMM - reconstruct, an fp16 GEMM with fp32 accumulation by hipBLASLt through torch.matmul
     (with tuned_gemm, the solution GEMM_TABLE records for its shape), then the output rotation
     (exl3_prefill_out_rotate) - kept as a comparison form, not taken by "auto"."""
@@ -372,7 +370,7 @@ def prefill_gemm(xh: torch.Tensor, trellis: torch.Tensor, k: int, n: int, K: int
         _check_out(out, (rows, n), out_dtype)
         _require(not _overlap(out, xh), "prefill_gemm: out must not overlap xh")
     if path == "auto":
-        path = "matmul" if k % 64 == 0 and prefill_matmul_fills_gpu(rows, n) else "fused"
+        path = "matmul" if k % 64 == 0 else "fused"
     if path in ("matmul", "library"):
         wt = torch.empty((n, k), dtype=torch.float16, device=xh.device)
         check(lib().exl3_reconstruct(ptr(trellis), k, n, K, cb, 0, n // 16, ptr(wt), stream_handle(xh.device)),

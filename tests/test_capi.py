@@ -88,15 +88,24 @@ def test_argument_errors(capi):
     assert lib.exl3_rmsnorm_rotate(p, None, None, p, 2, 1e-6, p, 1, 1, 128, p, p, None) == -1
     assert lib.exl3_swiglu_rotate(p, p, 1, 100, p, None) == -1
     assert lib.exl3_prefill_gemm(p, p, 64, 100, 6, 0, p, None, p, 0, 4, None) == -1
-    # hand-written prefill GEMM: k % 64, n % 128, rows, NULL, alignment, out dtype, 2 GiB operands
-    mm = lib.exl3_prefill_matmul
-    assert mm(p, p, 4, 96, 128, p, None, p, 0, None) == -1 and "multiple of 64" in _err(capi)
-    assert mm(p, p, 4, 64, 100, p, None, p, 0, None) == -1 and "multiple of 128" in _err(capi)
-    assert mm(p, p, 0, 64, 128, p, None, p, 0, None) == -1 and "rows" in _err(capi)
-    assert mm(None, p, 4, 64, 128, p, None, p, 0, None) == -1 and "NULL" in _err(capi)
-    assert mm(ctypes.c_void_p(0x1008), p, 4, 64, 128, p, None, p, 0, None) == -1 and "aligned" in _err(capi)
-    assert mm(p, p, 4, 64, 128, p, None, p, 3, None) == -1 and "out_dtype" in _err(capi)
-    assert mm(p, p, 1 << 20, 1024, 128, p, None, p, 0, None) == -1 and "2 GiB" in _err(capi)
+    # hand-written prefill GEMM: k % 64, n % 128, rows, NULL, alignment, out dtype, 2 GiB operands, workspace
+    def mm(xh, wt, rows, k, n, svh, bias, y, ot, ws=None, wsb=0):
+        return lib.exl3_prefill_matmul(xh, wt, rows, k, n, svh, bias, y, ot, ws, wsb, None)
+
+    assert mm(p, p, 4, 96, 128, p, None, p, 0) == -1 and "multiple of 64" in _err(capi)
+    assert mm(p, p, 4, 64, 100, p, None, p, 0) == -1 and "multiple of 128" in _err(capi)
+    assert mm(p, p, 0, 64, 128, p, None, p, 0) == -1 and "rows" in _err(capi)
+    assert mm(None, p, 4, 64, 128, p, None, p, 0) == -1 and "NULL" in _err(capi)
+    assert mm(ctypes.c_void_p(0x1008), p, 4, 64, 128, p, None, p, 0) == -1 and "aligned" in _err(capi)
+    assert mm(p, p, 4, 64, 128, p, None, p, 3) == -1 and "out_dtype" in _err(capi)
+    assert mm(p, p, 1 << 20, 1024, 128, p, None, p, 0) == -1 and "2 GiB" in _err(capi)
+    # few rows: k is split over workgroups, which needs the workspace the query reports
+    need = lib.exl3_prefill_matmul_workspace_bytes(9, 5120, 17408)
+    assert need > 0 and need % (9 * 17408 * 4) == 0   # whole fp32 (rows, n) arrays, one per split
+    assert mm(p, p, 9, 5120, 17408, p, None, p, 0) == -2 and "workspace" in _err(capi)
+    assert mm(p, p, 9, 5120, 17408, p, None, p, 0, p, need - 4) == -2
+    assert lib.exl3_prefill_matmul_workspace_bytes(4608, 5120, 17408) == 0   # the tiles fill the GPU: no split
+    assert lib.exl3_prefill_matmul_workspace_bytes(4608, 100, 17408) == 0    # invalid shape
     assert lib.exl3_codebook(3, 0, p, None) == -1
 
 

@@ -374,6 +374,32 @@ def test_prefill_matmul_tile_heights(pk, rows, n, k, ti, dt):
     assert ((y2.float() - ref0).abs().max() / ref0.abs().max()).item() < bar
 
 
+@pytest.mark.parametrize("rows,k,n", [(9, 5120, 17408), (9, 17408, 5120), (1, 5120, 1024), (64, 1024, 512),
+                                      (512, 6144, 5120)])
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16, torch.float32])
+def test_prefill_matmul_split_k(pk, rows, k, n, dt):
+    """Few rows: exl3_prefill_matmul splits k over several workgroups per tile (the workspace query is nonzero)
+    and a second launch adds the splits in order; against the fp32 torch product, with a bias, every output
+    dtype; deterministic."""
+    nbytes = pk._capi.lib().exl3_prefill_matmul_workspace_bytes(rows, k, n)
+    assert nbytes > 0 and nbytes % (rows * n * 4) == 0
+    print(f"prefill_matmul split rows {rows} k {k} n {n}: {nbytes // (rows * n * 4)} splits {dt}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(rows * 7 + k + n)
+    xh = (torch.randn((rows, k), device="cuda", generator=g) * 0.5).half()
+    wt = (torch.randn((n, k), device="cuda", generator=g) / math.sqrt(k)).half()
+    svh = (torch.randn(n, device="cuda", generator=g) * 0.1).half()
+    bias = (torch.randn(n, device="cuda", generator=g) * 0.1).to(dt)
+    y = torch.empty((rows, n), dtype=dt, device="cuda")
+    pk.kernels.prefill_matmul(xh, wt, svh, bias, y)
+    ref = (_had128_t(xh.float() @ wt.float().t()) * svh.float()).to(dt).float() + bias.float()
+    bar = 1e-2 if dt == torch.bfloat16 else 2e-3
+    err = ((y.float() - ref).abs().max() / ref.abs().max()).item()
+    assert err < bar, err
+    y2 = torch.empty_like(y)
+    pk.kernels.prefill_matmul(xh, wt, svh, bias, y2)
+    assert torch.equal(y, y2)
+
+
 def test_prefill_out_rotate_vs_torch_and_rejects(pk):
     """The output rotation alone: fp16(H128(g)/sqrt(128) * svh) per 128-column block, bit-exact against the
     rotation written in torch (fp32 butterflies in the same stage order); bad shapes are refused."""
