@@ -532,7 +532,7 @@ def main() -> int:
         "decode_tok_s": None,
     }
     log(f"GEMV: {value:.1f} GB/s whole job, kernel {kernel_gbs:.1f} GB/s")
-    del layers, evs, graph
+    del layers, graph
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
     if not args.no_configs:
