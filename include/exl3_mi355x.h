@@ -211,11 +211,11 @@ int exl3_prefill_matmul(const uint16_t* xh, const uint16_t* w_t, int rows, int k
  * entry point then rejects). */
 size_t exl3_prefill_matmul_workspace_bytes(int rows, int k, int n);
 
-/* Output rotation of the large-row prefill form, which is built as the reference's prefill is
- * (linear.py:97-105): exl3_reconstruct writes W_inner^T (bit-exact fp16), the caller multiplies
- * g = xh @ W_inner in fp16 with fp32 accumulation using its BLAS library (a plain library GEMM), and this
- * entry point replaces the reference's hadamard_transform(g) * svh: y = fp16(H128(g)/sqrt(128) * svh)
- * (+ bias) per 128-column block, in the output dtype.
+/* Output rotation for a prefill whose GEMM runs elsewhere (the package's "library" comparison form, built as
+ * the reference's prefill is, linear.py:97-105): exl3_reconstruct writes W_inner^T (bit-exact fp16), the
+ * caller multiplies g = xh @ W_inner in fp16 with fp32 accumulation using its BLAS library, and this entry
+ * point replaces the reference's hadamard_transform(g) * svh: y = fp16(H128(g)/sqrt(128) * svh) (+ bias) per
+ * 128-column block, in the output dtype. (exl3_prefill_matmul does the GEMM and this rotation in one launch.)
  *   g fp16 (rows, n) and svh fp16 [n], 16-byte aligned; bias NULL or [n] in out_dtype; y (rows, n) in
  *   out_dtype, 16-byte aligned (32 for fp32).
  *   n % 128 == 0, rows >= 1. */
