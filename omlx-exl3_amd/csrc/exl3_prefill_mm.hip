@@ -436,6 +436,7 @@ using namespace exl3;
 
 extern "C" size_t exl3_prefill_matmul_workspace_bytes(int rows, int k, int n) {
   if (rows < 1 || k < kMmBK || k % kMmBK != 0 || n < 128 || n % 128 != 0) return 0;
+  if ((uint64_t)((rows + 127) / 128) * (uint64_t)((n + kMmBN - 1) / kMmBN) >= (1ull << 31)) return 0;
   return mm_workspace_bytes(mm_plan(rows, k, n), rows, n);
 }
 
@@ -449,9 +450,11 @@ extern "C" int exl3_prefill_matmul(const uint16_t* xh, const uint16_t* w_t, int 
   EXL3_REQUIRE(out_dtype >= 0 && out_dtype <= 2, EXL3_ERR_ARG, "exl3_prefill_matmul: bad out_dtype %d", out_dtype);
   EXL3_REQUIRE(aligned(xh, 16) && aligned(w_t, 16) && aligned(y, 16), EXL3_ERR_ARG,
                "exl3_prefill_matmul: xh, w_t and y must be 16-byte aligned");
-  // (operands below 2 GiB keep every byte offset in 32 bits and the tile count in an int)
+  // (operands below 2 GiB keep every byte offset in 32 bits)
   EXL3_REQUIRE((uint64_t)rows * (uint64_t)k * 2u < (1ull << 31) && (uint64_t)n * (uint64_t)k * 2u < (1ull << 31),
                EXL3_ERR_ARG, "exl3_prefill_matmul: an operand exceeds 2 GiB");
+  EXL3_REQUIRE((uint64_t)((rows + 127) / 128) * (uint64_t)((n + kMmBN - 1) / kMmBN) < (1ull << 31), EXL3_ERR_ARG,
+               "exl3_prefill_matmul: too many tiles");
   const MmPlan p = mm_plan(rows, k, n);
   const size_t need = mm_workspace_bytes(p, rows, n);
   EXL3_REQUIRE(need == 0 || (workspace && workspace_bytes >= need && aligned(workspace, 16)), EXL3_ERR_WORKSPACE,

@@ -99,6 +99,7 @@ def test_argument_errors(capi):
     assert mm(ctypes.c_void_p(0x1008), p, 4, 64, 128, p, None, p, 0) == -1 and "aligned" in _err(capi)
     assert mm(p, p, 4, 64, 128, p, None, p, 3) == -1 and "out_dtype" in _err(capi)
     assert mm(p, p, 1 << 20, 1024, 128, p, None, p, 0) == -1 and "2 GiB" in _err(capi)
+    assert mm(p, p, 1 << 23, 64, 1 << 23, p, None, p, 0) == -1 and "tiles" in _err(capi)   # 2^31 tiles
     # few rows: k is split over workgroups, which needs the workspace the query reports
     need = lib.exl3_prefill_matmul_workspace_bytes(9, 5120, 17408)
     assert need > 0 and need % (9 * 17408 * 4) == 0   # whole fp32 (rows, n) arrays, one per split
