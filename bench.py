@@ -168,10 +168,12 @@ PROJ = [("q", 5120, 6144), ("k", 5120, 1024), ("v", 5120, 1024), ("o", 6144, 512
         ("up", 5120, 17408), ("down", 17408, 5120)]
 
 
-def mixed_k_benchmark(pk, torch, dev, rows_list=(1, 2, 4, 8), n_layers=8, reps=4) -> dict:
+def mixed_k_benchmark(pk, torch, dev, rows_list=(1, 2, 4, 8), n_layers=8, reps=10) -> dict:
     """Config 3: the 27B projections with K drawn per tensor from {2, 3, 4, 5, 6, 8} (seeded), siblings of
     equal K grouped as the loader groups them, at batch rows 1, 2, 4, 8. Layers rotate over a working set
-    beyond the Infinity Cache; GB/s = algorithmic bytes (at the drawn K) / time, launches timed back to back."""
+    beyond the Infinity Cache; GB/s = algorithmic bytes (at the drawn K) / time. All launches of a row count are
+    replayed from one HIP graph (back to back, no host dispatch between them); per K, that K's launches are
+    replayed from a graph of their own."""
     import random
     rnd = random.Random(3)
     g = torch.Generator(device=dev).manual_seed(77)
@@ -205,36 +207,49 @@ def mixed_k_benchmark(pk, torch, dev, rows_list=(1, 2, 4, 8), n_layers=8, reps=4
                 o = torch.empty((rows, sum(ns)), dtype=torch.float16, device=dev)
                 items.append((plan, xh, trs, o))
                 nbytes += algorithmic_bytes(k, ns, K, rows)
-        for plan, xh, trs, o in items:
-            plan(xh, trs, out=o)
-        torch.cuda.synchronize()
-        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        s.record()
-        for _ in range(reps):
-            for plan, xh, trs, o in items:
-                plan(xh, trs, out=o)
-        e.record()
-        torch.cuda.synchronize()
-        ms = s.elapsed_time(e) / reps
-        # per K: single launches bracketed by events, median over the repetitions
-        evs = []
-        for _ in range(reps):
-            for i, (plan, xh, trs, o) in enumerate(items):
-                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                a.record()
-                plan(xh, trs, out=o)
-                b.record()
-                evs.append((i, a, b))
-        torch.cuda.synchronize()
+        cap = torch.cuda.Stream(device=dev)
+
+        def graph_of(sel):
+            """The selected launches captured in one HIP graph (an eager pass on the capture stream first)."""
+            cap.wait_stream(torch.cuda.current_stream(dev))
+            with torch.cuda.stream(cap):
+                for plan, xh, trs, o in sel:
+                    plan(xh, trs, out=o)
+            torch.cuda.current_stream(dev).wait_stream(cap)
+            torch.cuda.synchronize()
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr):
+                for plan, xh, trs, o in sel:
+                    plan(xh, trs, out=o)
+            return gr
+
+        def time_graph(gr):
+            """ms per replay: HIP events on the replay stream around `reps` back-to-back replays."""
+            for _ in range(2):
+                gr.replay()
+            torch.cuda.synchronize()
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record()
+            for _ in range(reps):
+                gr.replay()
+            e.record()
+            torch.cuda.synchronize()
+            return s.elapsed_time(e) / reps
+
+        # every layer's launches back to back in one graph (no host dispatch between launches)
+        graph = graph_of(items)
+        ms = time_graph(graph)
+        del graph
+        # per K: that K's launches of all layers in one graph
         times = {}
-        for i, a, b in evs:
-            times.setdefault(i, []).append(a.elapsed_time(b))
+        for K in sorted({plan.K for plan, _x, _t, _o in items}):
+            sel = [it for it in items if it[0].K == K]
+            gr = graph_of(sel)
+            times[K] = (time_graph(gr), sel)
+            del gr
         per_k = {}
-        for i, (plan, _xh, _trs, _o) in enumerate(items):
-            d = per_k.setdefault(plan.K, [0, 0.0, 0])
-            d[0] += algorithmic_bytes(plan.k, plan.ns, plan.K, rows)
-            d[1] += statistics.median(times[i])
-            d[2] += 1
+        for K, (ms_k, sel) in times.items():
+            per_k[K] = [sum(algorithmic_bytes(p.k, p.ns, p.K, rows) for p, _x, _t, _o in sel), ms_k, len(sel)]
         out["per_rows"][str(rows)] = {
             "us_per_layer": round(ms * 1e3 / n_layers, 1), "GB_s": round(nbytes / ms / 1e6, 1),
             "pct_hbm_peak": round(100 * nbytes / ms / 1e6 / HBM_PEAK_GBS, 1),
@@ -244,38 +259,59 @@ def mixed_k_benchmark(pk, torch, dev, rows_list=(1, 2, 4, 8), n_layers=8, reps=4
     return out
 
 
-def prefill_benchmark(pk, torch, dev, rows=4608, reps=3) -> dict:
+def prefill_benchmark(pk, torch, dev, rows=4608, reps=6) -> dict:
     """Config 4: M = 4608 rotated fp16 activations through gate / up (5120 -> 17408) and down (17408 -> 5120)
     at K = 6. Three prefill forms are timed: "matmul" (W_inner^T reconstructed once, then the hand-written MFMA
     GEMM with the output rotation in its epilogue), "fused" (trellis tiles reconstructed in LDS, MFMA, Hadamard
     epilogue, one launch) and "library" (reconstruct, hipBLASLt fp16 GEMM with the tabled solution, output
     rotation: the reference's structure on the platform BLAS, for comparison); the headline figures are those
-    of the form prefill_gemm picks at this row count ("auto"). TFLOP/s = 2 M k n / time, against the 2.5
-    PFLOP/s dense fp16 MFMA peak."""
+    of the form prefill_gemm picks at this row count ("auto"). Every form first runs twice over the three
+    projections (warm clocks, allocator, plans); a form's figure is then the GPU time of `reps` back-to-back
+    passes over gate, up and down (HIP events, the region starting behind one more untimed pass so the GPU is
+    busy when it opens); per projection the same with that projection alone. TFLOP/s = 2 M k n / time,
+    against the 2.5 PFLOP/s dense fp16 MFMA peak."""
     g = torch.Generator(device=dev).manual_seed(5)
     paths = ("matmul", "fused", "library")
-    per = {p: {} for p in paths}
-    tot = {p: [0.0, 0.0] for p in paths}
-    for name, k, n in (("gate", 5120, 17408), ("up", 5120, 17408), ("down", 17408, 5120)):
+    shapes = (("gate", 5120, 17408), ("up", 5120, 17408), ("down", 17408, 5120))
+    data = {}
+    for name, k, n in shapes:
         tr = torch.randint(-32768, 32768, (k // 16, n // 16, 96), dtype=torch.int16, device=dev, generator=g)
         svh = torch.where(torch.rand(n, device=dev, generator=g) < 0.5, -1.0, 1.0).half()
         xh = torch.randn((rows, k), device=dev, generator=g).half()
         out = torch.empty((rows, n), dtype=torch.float16, device=dev)
-        for path in paths:
-            pk.kernels.prefill_gemm(xh, tr, k, n, 6, 0, svh, out=out, path=path)
-            torch.cuda.synchronize()
-            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            s.record()
-            for _ in range(reps):
-                pk.kernels.prefill_gemm(xh, tr, k, n, 6, 0, svh, out=out, path=path)
-            e.record()
-            torch.cuda.synchronize()
-            ms = s.elapsed_time(e) / reps
-            flop = 2.0 * rows * k * n
-            per[path][name] = {"ms": round(ms, 3), "TFLOP_s": round(flop / ms / 1e9, 1)}
-            tot[path][0] += flop
-            tot[path][1] += ms
-        del tr, xh, out
+        data[name] = (k, n, tr, svh, xh, out)
+
+    def call(name, path):
+        k, n, tr, svh, xh, out = data[name]
+        pk.kernels.prefill_gemm(xh, tr, k, n, 6, 0, svh, out=out, path=path)
+
+    def timed(names, path):
+        for nm in names:   # left running while the timed calls are queued
+            call(nm, path)
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(reps):
+            for nm in names:
+                call(nm, path)
+        e.record()
+        torch.cuda.synchronize()
+        return s.elapsed_time(e) / reps
+
+    flop = {name: 2.0 * rows * k * n for name, k, n in shapes}
+    names = [sh[0] for sh in shapes]
+    per, tot = {}, {}
+    for path in paths:
+        for _ in range(2):
+            for nm in names:
+                call(nm, path)
+        torch.cuda.synchronize()
+        ms_all = timed(names, path)
+        tot[path] = (sum(flop.values()), ms_all)
+        per[path] = {}
+        for nm in names:
+            ms = timed([nm], path)
+            per[path][nm] = {"ms": round(ms, 3), "TFLOP_s": round(flop[nm] / ms / 1e9, 1)}
+    del data
     auto = "matmul"   # prefill_gemm's "auto" path for these shapes (k a multiple of 64)
     tf = {p: tot[p][0] / tot[p][1] / 1e9 for p in tot}
     return {"rows": rows, "path": auto, "per_proj": per[auto], "TFLOP_s": round(tf[auto], 1),

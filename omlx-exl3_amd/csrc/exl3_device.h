@@ -405,9 +405,88 @@ __device__ __forceinline__ void store8(void* base, size_t i0, const float (&v)[8
   }
 }
 
+// ------------------------------------------------------------------------------------------------
+// lane exchanges on the VALU (no LDS round trip)
+// ------------------------------------------------------------------------------------------------
+// v from lane (lane ^ H) of the same 16-lane row, H = 1, 2, 4, 8, by DPP moves:
+// quad_perm [1,0,3,2] and [2,3,0,1] for 1 and 2; row_half_mirror (lane ^ 7) then quad_perm [3,2,1,0] (^ 3) for 4;
+// row_mirror (lane ^ 15) then row_half_mirror (^ 7) for 8. Every lane reads a lane of its own row, so a row that
+// is active as a whole never reads an inactive lane (bound_ctrl never applies).
+template <int H>
+__device__ __forceinline__ float lane_xor(float v) {
+  static_assert(H == 1 || H == 2 || H == 4 || H == 8, "lane_xor: in-row distances only");
+  auto dpp = [](int x, auto ctrl) { return __builtin_amdgcn_mov_dpp(x, decltype(ctrl)::value, 0xF, 0xF, true); };
+  const int x = __builtin_bit_cast(int, v);
+  int r;
+  if constexpr (H == 1) r = dpp(x, std::integral_constant<int, 0xB1>{});
+  else if constexpr (H == 2) r = dpp(x, std::integral_constant<int, 0x4E>{});
+  else if constexpr (H == 4) r = dpp(dpp(x, std::integral_constant<int, 0x141>{}), std::integral_constant<int, 0x1B>{});
+  else r = dpp(dpp(x, std::integral_constant<int, 0x140>{}), std::integral_constant<int, 0x141>{});
+  return __builtin_bit_cast(float, r);
+}
+
+// The two values of lanes lane & ~H and lane | H (H = 16, 32), in both lanes of each pair: v_permlane16_swap /
+// v_permlane32_swap with both operands v. The whole wavefront must be active.
+template <int H>
+__device__ __forceinline__ void pair_values(float v, float& lo, float& hi) {
+  static_assert(H == 16 || H == 32, "pair_values: cross-row distances only");
+  const uint32_t x = __builtin_bit_cast(uint32_t, v);
+  if constexpr (H == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    lo = __builtin_bit_cast(float, (uint32_t)r[0]);
+    hi = __builtin_bit_cast(float, (uint32_t)r[1]);
+  } else {
+    const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    lo = __builtin_bit_cast(float, (uint32_t)r[0]);
+    hi = __builtin_bit_cast(float, (uint32_t)r[1]);
+  }
+}
+
+// v from lane (lane ^ H), H = 1 .. 32, on the VALU (the whole wavefront active for H = 16, 32).
+template <int H>
+__device__ __forceinline__ float xor_partner(float v, int lane) {
+  if constexpr (H < 16) {
+    return lane_xor<H>(v);
+  } else {
+    float lo, hi;
+    pair_values<H>(v, lo, hi);
+    return (lane & H) ? lo : hi;
+  }
+}
+
+// Sum of a double over the 64 lanes of a wavefront, every lane getting the total: butterfly partners at
+// distances 32, 16, ..., 1 (the order and pairing of a shuffle-xor reduction), exchanged as two 32-bit halves.
+__device__ __forceinline__ double wave_sum(double v, int lane) {
+  static_for<0, 6>([&](auto I) {
+    constexpr int h = 32 >> decltype(I)::value;
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const float lo = __builtin_bit_cast(float, (uint32_t)b), hi = __builtin_bit_cast(float, (uint32_t)(b >> 32));
+    const uint64_t pb = (uint64_t)__builtin_bit_cast(uint32_t, xor_partner<h>(lo, lane)) |
+                        ((uint64_t)__builtin_bit_cast(uint32_t, xor_partner<h>(hi, lane)) << 32);
+    v += __builtin_bit_cast(double, pb);
+  });
+  return v;
+}
+
+// One FWHT stage across lanes lane and lane ^ H of a wavefront: the lower lane of the pair gets a + b, the upper
+// a - b (a the lower lane's value, b the upper's), each rounded once as the two-operand add and subtract are
+// (fma(+-1, x, y) has one rounding). H = 1..8 by DPP within a 16-lane row, 16 and 32 by pair_values. The whole
+// wavefront must be active for H = 16, 32 (a whole 16-lane row for H <= 8).
+template <int H>
+__device__ __forceinline__ float butterfly(float v, int lane) {
+  const float sgn = (lane & H) ? -1.f : 1.f;
+  if constexpr (H < 16) {
+    return __builtin_fmaf(sgn, v, lane_xor<H>(v));
+  } else {
+    float lo, hi;
+    pair_values<H>(v, lo, hi);
+    return __builtin_fmaf(sgn, hi, lo);
+  }
+}
+
 // 128-point FWHT of the block held by the 16-lane group of this lane (8 consecutive elements per lane):
 // stages h = 1, 2, 4 in-lane, 8..64 across lanes (xor 1, 2, 4, 8), each as (a + b, a - b) in fp32, in the
-// order 1, 2, ..., 64 of the reference's FWHT (kernels.py:374-386).
+// order 1, 2, ..., 64 of the reference's FWHT (kernels.py:374-386). The 16-lane group must be active as a whole.
 __device__ __forceinline__ void fwht128_lane8(float (&e)[8], int lane) {
 #pragma unroll
   for (int h = 1; h < 8; h <<= 1) {
@@ -420,15 +499,11 @@ __device__ __forceinline__ void fwht128_lane8(float (&e)[8], int lane) {
       }
     }
   }
+  static_for<0, 4>([&](auto HB) {
+    constexpr int hl = 1 << decltype(HB)::value;
 #pragma unroll
-  for (int hl = 1; hl < 16; hl <<= 1) {
-    const bool upper = (lane & hl) != 0;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float p = __shfl_xor(e[i], hl);
-      e[i] = upper ? p - e[i] : e[i] + p;
-    }
-  }
+    for (int i = 0; i < 8; ++i) e[i] = butterfly<hl>(e[i], lane);
+  });
 }
 
 }  // namespace exl3

@@ -74,8 +74,7 @@ __device__ void stage_prologue(const GemvArgs& a, int m, int blk_in_member, int 
 #pragma unroll
         for (int i = 0; i < 8; ++i) ss += (double)hv[i] * (double)hv[i];
       }
-#pragma unroll
-      for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+      ss = wave_sum(ss, lane);
       if (lane == 0) ss_part[r][wave] = ss;
     }
     __syncthreads();
@@ -195,8 +194,7 @@ __device__ void prologue_finish(const GemvArgs& a, const ProPre& p, int kt0, int
   for (int idx = nkt * RW + tid; idx < (nrec + 1) * RW; idx += nthr) xs[idx] = u32x4{0u, 0u, 0u, 0u};
   if (a.pro == kProNorm) {
     double ss = p.ss;
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+    ss = wave_sum(ss, lane);
     if (lane == 0) ss_part[0][wave] = ss;
     __syncthreads();
     if (tid == 0) {
@@ -436,6 +434,21 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(5))) void g
 
   if (prio) __builtin_amdgcn_s_setprio(0);
 
+  // the epilogue's per-column operands of this lane's two output columns: issued by the workgroup that writes
+  // y, next to the partial-sum loads (after the arrival: issued before it they would hold up every
+  // workgroup's store acknowledgement wait)
+  const int col_ep = blk * 128 + 2 * lane;
+  uint16_t svh_0 = 0, svh_1 = 0;
+  float bias0 = 0.f, bias1 = 0.f;
+  auto load_epilogue_operands = [&]() {
+    svh_0 = a.svh[col_ep];
+    svh_1 = a.svh[col_ep + 1];
+    if (a.bias) {
+      bias0 = load_as_f32<OT>(a.bias, col_ep);
+      bias1 = load_as_f32<OT>(a.bias, col_ep + 1);
+    }
+  };
+
   // ---- columns of this wavefront -> block partial (LDS), k-groups added in order 0, 1, .., WK-1 ----
   const int col_lo = (cw * 2 + (c >> 3)) * 16 + g, col_hi = col_lo + 8;
   for (int t = 0; t < WK; ++t) {
@@ -474,15 +487,19 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(5))) void g
     }
     __syncthreads();
     if (last == 0) return;
+    load_epilogue_operands();
     for (int idx = tid; idx < rows * 128; idx += nthr) {
       const int r = idx >> 7, cc = idx & 127;
       bv[r][cc] = sum_splits(part + (size_t)r * a.n_total + blk * 128 + cc, pstride, a.S);
     }
     if (tid == 0) __hip_atomic_store(&a.counters[(size_t)blk * kCounterStride], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
+  } else {
+    load_epilogue_operands();
   }
 
   // ---- 128-point FWHT per row (stages 1, 2, ..., 64), 1/sqrt(128), svh, bias ----
+  // (a wavefront's rows are uniform, so its 64 lanes are all active for the lane exchanges)
   for (int r = wave; r < rows; r += nthr >> 6) {
     float v0 = bv[r][2 * lane], v1 = bv[r][2 * lane + 1];
     {
@@ -490,25 +507,19 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(5))) void g
       v0 = s0;
       v1 = d0;
     }
-#pragma unroll
-    for (int h = 1; h < 64; h <<= 1) {
-      const float p0 = __shfl_xor(v0, h), p1 = __shfl_xor(v1, h);
-      if (lane & h) {
-        v0 = p0 - v0;
-        v1 = p1 - v1;
-      } else {
-        v0 = v0 + p0;
-        v1 = v1 + p1;
-      }
-    }
-    const int col = blk * 128 + 2 * lane;
-    float y0 = v0 * kHadScale * f16_to_f32(a.svh[col]);
-    float y1 = v1 * kHadScale * f16_to_f32(a.svh[col + 1]);
+    static_for<0, 6>([&](auto HB) {
+      constexpr int h = 1 << decltype(HB)::value;
+      v0 = butterfly<h>(v0, lane);
+      v1 = butterfly<h>(v1, lane);
+    });
+    const int col = col_ep;
+    float y0 = v0 * kHadScale * f16_to_f32(svh_0);
+    float y1 = v1 * kHadScale * f16_to_f32(svh_1);
     y0 = round_through<OT>(y0);
     y1 = round_through<OT>(y1);
     if (a.bias) {
-      y0 = round_through<OT>(y0 + load_as_f32<OT>(a.bias, col));
-      y1 = round_through<OT>(y1 + load_as_f32<OT>(a.bias, col + 1));
+      y0 = round_through<OT>(y0 + bias0);
+      y1 = round_through<OT>(y1 + bias1);
     }
     const size_t o = (size_t)r * a.n_total + col;
     if (a.eres) {   // residual add of the next RMSNorm (fp16 output)
@@ -519,8 +530,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(5))) void g
     store_from_f32<OT>(a.y, o + 1, y1);
     if (a.ess) {    // this block's sum of squares for the next RMSNorm
       double ss = (double)y0 * (double)y0 + (double)y1 * (double)y1;
-#pragma unroll
-      for (int h = 32; h >= 1; h >>= 1) ss += __shfl_xor(ss, h);
+      ss = wave_sum(ss, lane);
       if (lane == 0) a.ess[(size_t)r * (a.n_total / 128) + blk] = ss;
     }
   }

@@ -132,17 +132,20 @@ constexpr int kDepth = 2;
 
 
 // Sum of S split partials src[0], src[stride], ..., in split order, read with device-scope loads. The loads
-// are issued eight at a time before any is used, so the sum costs ceil(S / 8) memory round trips, not S.
+// are issued sixteen at a time before any is used (indices past S re-read the last partial, so the issue has no
+// branches), and the sum costs ceil(S / 16) memory round trips, not S.
+constexpr int kSplitBatch = 16;
 __device__ __forceinline__ float sum_splits(const float* src, size_t stride, int S) {
   float v = 0.f;
-  for (int s0 = 0; s0 < S; s0 += 8) {
-    float t[8];
+  for (int s0 = 0; s0 < S; s0 += kSplitBatch) {
+    float t[kSplitBatch];
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
-      t[u] = s0 + u < S ? __hip_atomic_load(src + (size_t)(s0 + u) * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                        : 0.f;
+    for (int u = 0; u < kSplitBatch; ++u) {
+      const int su = s0 + u < S ? s0 + u : S - 1;
+      t[u] = __hip_atomic_load(src + (size_t)su * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
+    for (int u = 0; u < kSplitBatch; ++u)
       if (s0 + u < S) v += t[u];
   }
   return v;
@@ -152,17 +155,17 @@ __device__ __forceinline__ float sum_splits(const float* src, size_t stride, int
 __device__ __forceinline__ void sum_splits2(const float* src, size_t stride, int S, float& v0, float& v1) {
   v0 = 0.f;
   v1 = 0.f;
-  for (int s0 = 0; s0 < S; s0 += 8) {
-    float t0[8], t1[8];
+  for (int s0 = 0; s0 < S; s0 += kSplitBatch) {
+    float t0[kSplitBatch], t1[kSplitBatch];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const bool ok = s0 + u < S;
-      const float* p = src + (size_t)(ok ? s0 + u : 0) * stride;
-      t0[u] = ok ? __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
-      t1[u] = ok ? __hip_atomic_load(p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
+    for (int u = 0; u < kSplitBatch; ++u) {
+      const int su = s0 + u < S ? s0 + u : S - 1;
+      const float* p = src + (size_t)su * stride;
+      t0[u] = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      t1[u] = __hip_atomic_load(p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
+    for (int u = 0; u < kSplitBatch; ++u)
       if (s0 + u < S) {
         v0 += t0[u];
         v1 += t1[u];

@@ -228,17 +228,11 @@ __global__ __launch_bounds__(kLutThreads) void gemv_lut_kernel(GemvLutArgs a) {
       v0 = s0;
       v1 = d0;
     }
-#pragma unroll
-    for (int h = 1; h < 64; h <<= 1) {
-      const float p0 = __shfl_xor(v0, h), p1 = __shfl_xor(v1, h);
-      if (lane & h) {
-        v0 = p0 - v0;
-        v1 = p1 - v1;
-      } else {
-        v0 = v0 + p0;
-        v1 = v1 + p1;
-      }
-    }
+    static_for<0, 6>([&](auto HB) {   // the wavefront is active as a whole here
+      constexpr int h = 1 << decltype(HB)::value;
+      v0 = butterfly<h>(v0, lane);
+      v1 = butterfly<h>(v1, lane);
+    });
     float y0 = round_through<OT>(v0 * kHadScale * sv0), y1 = round_through<OT>(v1 * kHadScale * sv1);
     if (a.bias) {
       y0 = y0 + b0;

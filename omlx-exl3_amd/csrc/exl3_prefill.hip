@@ -199,15 +199,11 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const uint16_t* __r
       float v[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) v[j] = acc[i][j][r];
+      static_for<0, 4>([&](auto HB) {
+        constexpr int h = 1 << decltype(HB)::value;
 #pragma unroll
-      for (int h = 1; h < 16; h <<= 1) {
-        const bool upper = (c & h) != 0;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float p = __shfl_xor(v[j], h);
-          v[j] = upper ? p - v[j] : v[j] + p;
-        }
-      }
+        for (int j = 0; j < 8; ++j) v[j] = butterfly<h>(v[j], c);
+      });
 #pragma unroll
       for (int hj = 1; hj < 8; hj <<= 1) {
 #pragma unroll

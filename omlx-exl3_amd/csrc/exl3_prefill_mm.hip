@@ -33,22 +33,6 @@ constexpr int kMmThreads = 512, kMmWaves = kMmThreads / 64;
 // contiguous runs, which are conflict-free too.
 __device__ __forceinline__ int mm_pos(int r, int p) { return p ^ (r & 7); }
 __device__ __forceinline__ int mm_slot(int r, int p) { return r * (kMmBK / 8) + mm_pos(r, p); }
-// v from lane (lane ^ H) of the same 16-lane row, H = 1, 2, 4, 8, by DPP moves (VALU, no LDS round trip):
-// quad_perm [1,0,3,2] and [2,3,0,1] for 1 and 2; row_half_mirror (lane ^ 7) then quad_perm [3,2,1,0] (^ 3) for 4;
-// row_mirror (lane ^ 15) then row_half_mirror (^ 7) for 8.
-template <int H>
-__device__ __forceinline__ float row_xor(float v) {
-  // (every lane reads a lane of its own row, so bound_ctrl never applies; mov_dpp has no old-value operand to copy)
-  auto dpp = [](int x, auto ctrl) { return __builtin_amdgcn_mov_dpp(x, decltype(ctrl)::value, 0xF, 0xF, true); };
-  const int x = __builtin_bit_cast(int, v);
-  int r;
-  if constexpr (H == 1) r = dpp(x, std::integral_constant<int, 0xB1>{});
-  else if constexpr (H == 2) r = dpp(x, std::integral_constant<int, 0x4E>{});
-  else if constexpr (H == 4) r = dpp(dpp(x, std::integral_constant<int, 0x141>{}), std::integral_constant<int, 0x1B>{});
-  else r = dpp(dpp(x, std::integral_constant<int, 0x140>{}), std::integral_constant<int, 0x141>{});
-  return __builtin_bit_cast(float, r);
-}
-
 // instruction classes of __builtin_amdgcn_sched_group_barrier
 constexpr int kSchedMfma = 0x008, kSchedVmemRead = 0x020, kSchedDsRead = 0x100;
 
@@ -276,7 +260,7 @@ __global__ __launch_bounds__(kMmThreads) __attribute__((amdgpu_waves_per_eu(2)))
         constexpr int h = 1 << decltype(HB)::value;
         const float sgn = (c & h) ? -1.f : 1.f;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = __builtin_fmaf(sgn, v[j], row_xor<h>(v[j]));
+        for (int j = 0; j < 8; ++j) v[j] = __builtin_fmaf(sgn, v[j], lane_xor<h>(v[j]));
       });
 #pragma unroll
       for (int hj = 1; hj < 8; hj <<= 1) {

@@ -86,8 +86,7 @@ __global__ __launch_bounds__(256) void norm_rot_kernel(const void* __restrict__ 
 #pragma unroll
     for (int i = 0; i < 8; ++i) ss += (double)hv[i] * (double)hv[i];
   }
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+  ss = wave_sum(ss, lane);
   if (lane == 0) part[wave] = ss;
   __syncthreads();
   const double tot = ((part[0] + part[1]) + part[2]) + part[3];
