@@ -20,8 +20,9 @@ timing starts.
                  all layers in one graph, replayed, events around the replays / launches (as the headline)
   cpu_baseline   the NumPy oracle (reconstruct + fp32 matmul + Hadamard + svh) on the q projection
   mixed_k        config 3: the 27B projections with K drawn per tensor from {2,3,4,5,6,8}, rows 1 / 2 / 4 / 8,
-                 whole layers back to back, and per K the GB/s of that K's launches (medians of single
-                 launches, so each includes its dispatch latency)
+                 whole layers replayed from a HIP graph with siblings grouped as the loader groups them (one
+                 q/k/v and one gate/up launch whatever their K); split_by_K: the same tensors grouped the
+                 reference's way (equal K only), with the GB/s of each K's launches
   prefill        config 4: M = 4608 through gate / up / down at K = 6, TFLOP/s against the fp16 MFMA peak
   decode_tok_s   end-to-end batch-1 greedy decode of the synthetic 27B-shape EXL3 decoder (config 5: 64
                  layers, hidden 5120, MLP 17408, GQA 48/8 x 128, head 5120 -> 151936, K = 6): a 512-token
@@ -163,99 +164,115 @@ def cpu_baseline(seconds_budget: float = 30.0) -> dict:
 MFMA_F16_PEAK_TFLOPS = 2500.0
 # weight bytes read per decode token of the 64-layer 27B-shape decoder at K = 6 (layers' trellis + head)
 DECODE_BYTES_PER_TOKEN = 64 * 255_590_400 + 583_434_240
-# 27B projections as separate tensors (a mixed-bitrate checkpoint groups only siblings of equal K)
+# 27B projections as separate tensors (their K drawn per tensor in the mixed-bitrate configuration)
 PROJ = [("q", 5120, 6144), ("k", 5120, 1024), ("v", 5120, 1024), ("o", 6144, 5120), ("gate", 5120, 17408),
         ("up", 5120, 17408), ("down", 17408, 5120)]
 
 
 def mixed_k_benchmark(pk, torch, dev, rows_list=(1, 2, 4, 8), n_layers=8, reps=10) -> dict:
-    """Config 3: the 27B projections with K drawn per tensor from {2, 3, 4, 5, 6, 8} (seeded), siblings of
-    equal K grouped as the loader groups them, at batch rows 1, 2, 4, 8. Layers rotate over a working set
-    beyond the Infinity Cache; GB/s = algorithmic bytes (at the drawn K) / time. All launches of a row count are
-    replayed from one HIP graph (back to back, no host dispatch between them); per K, that K's launches are
-    replayed from a graph of their own."""
+    """Config 3: the 27B projections with K drawn per tensor from {2, 3, 4, 5, 6, 8} (seeded), at batch rows 1,
+    2, 4, 8. Siblings are grouped as the loader groups them: q/k/v and gate/up are one launch each whatever
+    their K (the mixed-width GEMV). For comparison the same tensors are also run grouped the reference's way
+    (only siblings of equal K share a launch, loader.py:137-156), with GB/s per K from that form. Layers
+    rotate over a working set beyond the Infinity Cache; GB/s = algorithmic bytes (at the drawn K) / time. A
+    form's launches are replayed from one HIP graph (back to back, no host dispatch between them); per K,
+    that K's launches are replayed from a graph of their own."""
     import random
     rnd = random.Random(3)
     g = torch.Generator(device=dev).manual_seed(77)
+    shape = {name: (k, n) for name, k, n in PROJ}
+    sibsets = (("q", "k", "v"), ("gate", "up"), ("o",), ("down",))
     layers, draws = [], []
     for _ in range(n_layers):
         Ks = {name: rnd.choice([2, 3, 4, 5, 6, 8]) for name, _, _ in PROJ}
         draws.append(Ks)
-        groups = []
-        for sib in (("q", "k", "v"), ("gate", "up"), ("o",), ("down",)):
-            by_k = {}
-            for name in sib:
-                by_k.setdefault(Ks[name], []).append(name)
-            for K, names in by_k.items():
-                k = [p[1] for p in PROJ if p[0] == names[0]][0]
-                ns = [[p[2] for p in PROJ if p[0] == nm][0] for nm in names]
-                trs = [torch.randint(-32768, 32768, (k // 16, n // 16, 16 * K), dtype=torch.int16, device=dev,
-                                     generator=g) for n in ns]
-                svh = torch.where(torch.rand(sum(ns), device=dev, generator=g) < 0.5, -1.0, 1.0).half()
-                groups.append((k, ns, K, trs, svh))
-        layers.append(groups)
+        tens = {}
+        for name, (k, n) in shape.items():
+            tens[name] = (torch.randint(-32768, 32768, (k // 16, n // 16, 16 * Ks[name]), dtype=torch.int16,
+                                        device=dev, generator=g),
+                          torch.where(torch.rand(n, device=dev, generator=g) < 0.5, -1.0, 1.0).half())
+        layers.append((Ks, tens))
     out = {"draws": draws, "per_rows": {}}
     bpw = sum(K * k * n for Ks in draws for (name, k, n) in PROJ for K in [Ks[name]]) / \
         sum(k * n for _ in draws for (_, k, n) in PROJ)
     out["mean_bpw"] = round(bpw, 3)
-    for rows in rows_list:
+
+    def launches(rows, by_k):
+        """(plan, xh, trellises, out) per launch of every layer; by_k: the reference's grouping."""
         items, nbytes = [], 0
-        for groups in layers:
-            for k, ns, K, trs, svh in groups:
-                plan = pk.kernels.TrellisGemvPlan(k, ns, K, 0, svh, rows, torch.float16)
-                xh = torch.randn((len(ns), rows, k), device=dev, generator=g).half()
-                o = torch.empty((rows, sum(ns)), dtype=torch.float16, device=dev)
-                items.append((plan, xh, trs, o))
-                nbytes += algorithmic_bytes(k, ns, K, rows)
-        cap = torch.cuda.Stream(device=dev)
+        for Ks, tens in layers:
+            for sib in sibsets:
+                subsets = {}
+                for name in sib:
+                    subsets.setdefault(Ks[name] if by_k else 0, []).append(name)
+                for names in subsets.values():
+                    k = shape[names[0]][0]
+                    ns = [shape[nm][1] for nm in names]
+                    mKs = [Ks[nm] for nm in names]
+                    svh = torch.cat([tens[nm][1] for nm in names])
+                    plan = pk.kernels.TrellisGemvPlan(k, ns, mKs, 0, svh, rows, torch.float16)
+                    xh = torch.randn((len(ns), rows, k), device=dev, generator=g).half()
+                    o = torch.empty((rows, sum(ns)), dtype=torch.float16, device=dev)
+                    items.append((plan, xh, [tens[nm][0] for nm in names], o))
+                    nbytes += sum(algorithmic_bytes(k, [n], K, rows) for n, K in zip(ns, mKs))
+        return items, nbytes
 
-        def graph_of(sel):
-            """The selected launches captured in one HIP graph (an eager pass on the capture stream first)."""
-            cap.wait_stream(torch.cuda.current_stream(dev))
-            with torch.cuda.stream(cap):
-                for plan, xh, trs, o in sel:
-                    plan(xh, trs, out=o)
-            torch.cuda.current_stream(dev).wait_stream(cap)
-            torch.cuda.synchronize()
-            gr = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(gr):
-                for plan, xh, trs, o in sel:
-                    plan(xh, trs, out=o)
-            return gr
+    cap = torch.cuda.Stream(device=dev)
 
-        def time_graph(gr):
-            """ms per replay: HIP events on the replay stream around `reps` back-to-back replays."""
-            for _ in range(2):
-                gr.replay()
-            torch.cuda.synchronize()
-            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            s.record()
-            for _ in range(reps):
-                gr.replay()
-            e.record()
-            torch.cuda.synchronize()
-            return s.elapsed_time(e) / reps
+    def graph_of(sel):
+        """The selected launches captured in one HIP graph (an eager pass on the capture stream first)."""
+        cap.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(cap):
+            for plan, xh, trs, o in sel:
+                plan(xh, trs, out=o)
+        torch.cuda.current_stream(dev).wait_stream(cap)
+        torch.cuda.synchronize()
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            for plan, xh, trs, o in sel:
+                plan(xh, trs, out=o)
+        return gr
 
-        # every layer's launches back to back in one graph (no host dispatch between launches)
+    def time_graph(gr):
+        """ms per replay: HIP events on the replay stream around `reps` back-to-back replays."""
+        for _ in range(2):
+            gr.replay()
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(reps):
+            gr.replay()
+        e.record()
+        torch.cuda.synchronize()
+        return s.elapsed_time(e) / reps
+
+    def whole(items, nbytes):
         graph = graph_of(items)
         ms = time_graph(graph)
         del graph
-        # per K: that K's launches of all layers in one graph
-        times = {}
+        return {"launches_per_layer": round(len(items) / n_layers, 2), "us_per_layer": round(ms * 1e3 / n_layers, 1),
+                "GB_s": round(nbytes / ms / 1e6, 1), "pct_hbm_peak": round(100 * nbytes / ms / 1e6 / HBM_PEAK_GBS, 1)}
+
+    for rows in rows_list:
+        items, nbytes = launches(rows, by_k=False)
+        res = whole(items, nbytes)
+        del items
+        # the reference's grouping of the same tensors, and per K from it
+        items, nbytes = launches(rows, by_k=True)
+        split = whole(items, nbytes)
+        per_k = {}
         for K in sorted({plan.K for plan, _x, _t, _o in items}):
             sel = [it for it in items if it[0].K == K]
             gr = graph_of(sel)
-            times[K] = (time_graph(gr), sel)
+            ms_k = time_graph(gr)
             del gr
-        per_k = {}
-        for K, (ms_k, sel) in times.items():
-            per_k[K] = [sum(algorithmic_bytes(p.k, p.ns, p.K, rows) for p, _x, _t, _o in sel), ms_k, len(sel)]
-        out["per_rows"][str(rows)] = {
-            "us_per_layer": round(ms * 1e3 / n_layers, 1), "GB_s": round(nbytes / ms / 1e6, 1),
-            "pct_hbm_peak": round(100 * nbytes / ms / 1e6 / HBM_PEAK_GBS, 1),
-            "per_K": {str(K): {"launches": d[2], "GB_s": round(d[0] / d[1] / 1e6, 1),
-                               "pct_hbm_peak": round(100 * d[0] / d[1] / 1e6 / HBM_PEAK_GBS, 1)}
-                      for K, d in sorted(per_k.items())}}
+            nb = sum(algorithmic_bytes(p.k, p.ns, p.K, rows) for p, _x, _t, _o in sel)
+            per_k[str(K)] = {"launches": len(sel), "GB_s": round(nb / ms_k / 1e6, 1),
+                             "pct_hbm_peak": round(100 * nb / ms_k / 1e6 / HBM_PEAK_GBS, 1)}
+        del items
+        split["per_K"] = per_k
+        res["split_by_K"] = split
+        out["per_rows"][str(rows)] = res
     return out
 
 

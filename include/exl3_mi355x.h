@@ -157,6 +157,20 @@ int exl3_gemv_fused(int prologue, const uint16_t* x, const uint16_t* residual, u
                     const uint16_t* y_residual, double* y_sumsq, void* workspace, size_t workspace_bytes,
                     void* stream);
 
+/* exl3_gemv_fused for siblings of different bit widths: member m's trellis is at member_K[m] bits per weight
+ * (1..8; uint32 view of int16 [k/16, member_n[m]/16, 16 member_K[m]]), all members in one launch. No counterpart
+ * in the reference, whose sibling fusion takes only members of one bitrate (loader.py:137-156, linear.py:124-193)
+ * and runs the others as separate launches. Members of different K use the exact layout on the hashing kernel:
+ * flags EXL3_GEMV_FAST or EXL3_GEMV_TABLE are rejected (EXL3_ERR_ARG) unless every member_K is equal, in which case
+ * the call is exl3_gemv_fused with K = member_K[0]. The workspace is sized by exl3_gemv_workspace_bytes with any
+ * member's K. Other arguments, rounding and reduction order as exl3_gemv_fused. */
+int exl3_gemv_fused_mk(int prologue, const uint16_t* x, const uint16_t* residual, uint16_t* residual_out,
+                       uint16_t* xn_out, const uint16_t* w, float eps, const double* x_sumsq, const uint16_t* suh,
+                       const uint32_t* const* trellis, int n_members, const int* member_n, const int* member_K,
+                       int k, int cb, const uint16_t* svh, const void* bias, void* y, int out_dtype, int rows,
+                       unsigned flags, const uint16_t* y_residual, double* y_sumsq, void* workspace,
+                       size_t workspace_bytes, void* stream);
+
 /* Input rotation: xh[m, r, :] = fp16(H128(x[r, :] * suh[m, :]) / sqrt(128)) per 128-block, fp32 inside.
  * Replaces rot (kernels.py:388-406, 451-458). x (rows, k) in x_dtype; suh fp16 (n_members, k);
  * xh fp16 (n_members, rows, k). k % 128 == 0. xh must not overlap x or suh. */

@@ -31,6 +31,9 @@ _SIGNATURES = {
                                    _c_uint, _vp]),
     "exl3_gemv_fused": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _vp, _c_float, _vp, _vp, _vp, _c_int, _vp, _c_int, _c_int,
                                  _c_int, _vp, _vp, _vp, _c_int, _c_int, _c_uint, _vp, _vp, _vp, _c_size, _vp]),
+    "exl3_gemv_fused_mk": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _vp, _c_float, _vp, _vp, _vp, _c_int, _vp, _vp,
+                                    _c_int, _c_int, _vp, _vp, _vp, _c_int, _c_int, _c_uint, _vp, _vp, _vp, _c_size,
+                                    _vp]),
     "exl3_rotate": (_c_int, [_vp, _c_int, _vp, _c_int, _c_int, _c_int, _vp, _vp]),
     "exl3_rmsnorm_rotate": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _c_float, _vp, _c_int, _c_int, _c_int, _vp, _vp,
                                      _vp]),

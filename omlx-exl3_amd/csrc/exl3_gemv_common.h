@@ -13,6 +13,7 @@ struct GemvArgs {
   const uint16_t* xh;
   const uint32_t* tr[3];
   int NT[3];
+  int Km[3];                  // bits per weight of each member (read by the mixed-width kernel)
   int blk_end[3];
   const uint16_t* svh;
   const void* bias;
@@ -196,5 +197,18 @@ size_t gemv_lut_partials(int KT, int n_total, int rows);   // the partials' part
 bool gemv_lut_eligible(int k, int K, int cb, unsigned flags);
 bool gemv_lut_offsets_fit(int k, int n, int K);
 int gemv_lut_launch(GemvLutArgs& a, int K, int cb, int out_dtype, hipStream_t st);
+
+// staged activations: at most 26 iterations x 4 k-tiles x 16 rows x 64 B (+ zero record) = 104 KiB + 64 B
+constexpr size_t kMaxGemvSmem = 112 * 1024;
+
+// grid, block and stream of a GEMV launch (grid (blocks, S), S in GemvArgs)
+struct GemvLaunch {
+  int blocks, threads;
+  size_t smem;
+  hipStream_t st;
+};
+
+// Launch of the mixed-width kernel (exl3_gemv_mk.hip): codebook cb, output type ot, members' widths in a.Km.
+void gemv_launch_mk(int cb, int ot, const GemvArgs& a, int blocks, int threads, size_t smem, hipStream_t st);
 
 }  // namespace exl3

@@ -161,21 +161,31 @@ def swiglu_rot(gu: torch.Tensor, suh: torch.Tensor, out: torch.Tensor | None = N
 
 class TrellisGemvPlan:
     """y = had128(xh @ W_inner) * svh (+ bias) in out_dtype for one EXL3 linear or a sibling group of
-    <= 3 members sharing K and codebook (kernels.py:263-299). xh is (n_members, rows, k): each member's own
+    <= 3 members sharing the codebook (kernels.py:263-299). xh is (n_members, rows, k): each member's own
     rotated input. The plan owns the launch parameters and a zeroed workspace (split-K partials and
     per-block arrival counters that the kernel leaves at zero).
 
-    Kernels: the hashing kernel by default; table=True selects the table kernel (LDS codebook lookup for
-    half of each run) for exact contraction when k % 64 == 0. kt_per_split is a hashing-kernel knob."""
+    K is the members' bits per weight, or one value per member: members of different K still run as one
+    launch (exl3_gemv_fused_mk; the reference fuses only siblings of one bitrate, linear.py:124-193), in the
+    exact layout on the hashing kernel. Kernels: the hashing kernel by default; table=True selects the table
+    kernel (LDS codebook lookup for half of each run) for exact contraction when k % 64 == 0. kt_per_split is a
+    hashing-kernel knob (one K only)."""
 
-    def __init__(self, k: int, member_ns: list[int], K: int, cb: int, svh: torch.Tensor, rows: int,
+    def __init__(self, k: int, member_ns: list[int], K, cb: int, svh: torch.Tensor, rows: int,
                  out_dtype: torch.dtype = torch.float16, *, fast: bool = False, kt_per_split: int = 0,
                  table: bool = False):
-        _require(k % 16 == 0 and all(n % 128 == 0 for n in member_ns) and 1 <= K <= 8 and cb in (0, 1, 2),
-                 "TrellisGemvPlan: k % 16, n % 128, 1 <= K <= 8, codebook 0..2")
+        Ks = [int(x) for x in K] if isinstance(K, (list, tuple)) else [int(K)] * len(member_ns)
+        _require(len(Ks) == len(member_ns), "TrellisGemvPlan: one K per member")
+        _require(k % 16 == 0 and all(n % 128 == 0 for n in member_ns) and all(1 <= x <= 8 for x in Ks)
+                 and cb in (0, 1, 2), "TrellisGemvPlan: k % 16, n % 128, 1 <= K <= 8, codebook 0..2")
         _require(1 <= len(member_ns) <= 3 and 1 <= rows <= GEMV_ROWS_LIMIT, "TrellisGemvPlan: 1..3 members, rows")
         _require(out_dtype in DTYPE_CODE, "TrellisGemvPlan: out_dtype fp16, bf16 or fp32")
-        self.k, self.ns, self.n, self.K, self.cb, self.rows = k, list(member_ns), sum(member_ns), K, cb, rows
+        self.mixed = len(set(Ks)) > 1
+        _require(not (self.mixed and (fast or table or kt_per_split)),
+                 "TrellisGemvPlan: members of different K take the exact layout (no fast, table or kt_per_split)")
+        self.Ks = Ks
+        self.k, self.ns, self.n, self.cb, self.rows = k, list(member_ns), sum(member_ns), cb, rows
+        self.K = tuple(Ks) if self.mixed else Ks[0]
         self.out_dtype = out_dtype
         self.nsub = len(member_ns)
         self.flags = (GEMV_FAST if fast else GEMV_EXACT) | (GEMV_TABLE if table else 0)
@@ -183,7 +193,8 @@ class TrellisGemvPlan:
         self.svh = svh.to(torch.float16).reshape(-1).contiguous()
         _require(self.svh.numel() == self.n, "TrellisGemvPlan: svh must have sum(member_ns) elements")
         self.device = self.svh.device
-        nbytes = lib().exl3_gemv_workspace_bytes(k, self.n, rows, K)
+        self._Ks_c = (ctypes.c_int * 3)(*(Ks + [Ks[0]] * (3 - len(Ks))))
+        nbytes = lib().exl3_gemv_workspace_bytes(k, self.n, rows, max(Ks))
         if kt_per_split:
             KT = k // 16
             kps = (kt_per_split + 3) // 4 * 4
@@ -199,8 +210,8 @@ class TrellisGemvPlan:
         _require(len(trellises) == self.nsub, "one trellis per member")
         key = tuple(t.data_ptr() for t in trellises)
         if key != self._tr_key:
-            for t, n in zip(trellises, self.ns):
-                trellis_words(t, self.k, n, self.K)
+            for t, n, Km in zip(trellises, self.ns, self.Ks):
+                trellis_words(t, self.k, n, Km)
             self._tr_c = (ctypes.c_void_p * 3)(*(list(key) + [key[0]] * (3 - len(key))))
             self._tr_key = key
             self._tr_refs = list(trellises)
@@ -217,6 +228,8 @@ class TrellisGemvPlan:
         _dev(xh, "xh")
         _require(xh.dtype == torch.float16 and xh.numel() == self.nsub * self.rows * self.k,
                  f"xh must be fp16 ({self.nsub}, {self.rows}, {self.k})")
+        if self.mixed:
+            return self.fused(PROLOGUE_NONE, xh, trellises, bias=bias, out=out)
         out = self._bind(trellises, bias, out, xh.device)
         rc = lib().exl3_gemv_ex(ptr(xh), self._tr_c, self.nsub, self._ns_c, self.k, self.K, self.cb, ptr(self.svh),
                                 ptr(bias), ptr(out), DTYPE_CODE[self.out_dtype], self.rows, self.flags,
@@ -259,6 +272,15 @@ class TrellisGemvPlan:
                      "residual_out / xn_out must not overlap x, residual or weight")
         _require(not _overlap(residual_out, xn_out), "residual_out and xn_out must not overlap")
         out = self._bind(trellises, bias, out, x.device)
+        if self.mixed:
+            rc = lib().exl3_gemv_fused_mk(prologue, ptr(x), ptr(residual), ptr(residual_out), ptr(xn_out),
+                                          ptr(weight), float(eps), ptr(x_sumsq), ptr(suh), self._tr_c, self.nsub,
+                                          self._ns_c, self._Ks_c, self.k, self.cb, ptr(self.svh), ptr(bias), ptr(out),
+                                          DTYPE_CODE[self.out_dtype], self.rows, self.flags, ptr(y_residual),
+                                          ptr(y_sumsq), ptr(self.workspace), self.workspace.numel(),
+                                          stream_handle(x.device))
+            check(rc, "exl3_gemv_fused_mk")
+            return out
         rc = lib().exl3_gemv_fused(prologue, ptr(x), ptr(residual), ptr(residual_out), ptr(xn_out), ptr(weight),
                                    float(eps), ptr(x_sumsq), ptr(suh), self._tr_c, self.nsub, self._ns_c, self.k, self.K, self.cb,
                                    ptr(self.svh), ptr(bias), ptr(out), DTYPE_CODE[self.out_dtype], self.rows,

@@ -311,19 +311,24 @@ class EXL3Linear(nn.Module):
 
 
 class EXL3SiblingGroup:
-    """Same-input EXL3 siblings computed in one launch for rows <= MAX_GEMV_ROWS (linear.py:124-193)."""
+    """Same-input EXL3 siblings computed in one launch for rows <= MAX_GEMV_ROWS (linear.py:124-193). Unlike
+    the reference's groups, members may differ in bits per weight: one launch serves them all (the
+    mixed-width GEMV, exl3_gemv_fused_mk), so a mixed-bitrate checkpoint keeps one q/k/v and one gate/up
+    launch per layer."""
 
     def __init__(self, members: list[EXL3Linear]):
         for m in members:
             m._prepare()
         if not EXL3SiblingGroup.fusable(members):
-            raise ValueError("EXL3SiblingGroup: members must share in_features, K and codebook, have "
+            raise ValueError("EXL3SiblingGroup: members must share in_features and codebook, have "
                              "out_features % 128 == 0, no bias, and number 2..3")
         first = members[0]
         self.members = members
         self.k = first.in_features
         self.ns = [m.out_features for m in members]
-        self.K, self.cb = first._K, first._cb
+        self.Ks = [m._K for m in members]
+        self.K = self.Ks[0] if len(set(self.Ks)) == 1 else tuple(self.Ks)
+        self.cb = first._cb
         self.suh = torch.stack([m._suh for m in members]).contiguous()          # (n_members, k)
         self.svh = torch.cat([m._svh for m in members]).contiguous()
         self.trs = [m._tr for m in members]
@@ -342,7 +347,7 @@ class EXL3SiblingGroup:
             m._prepare()
         f = members[0]
         return (2 <= len(members) <= 3
-                and all(m.in_features == f.in_features and m._K == f._K and m._cb == f._cb for m in members)
+                and all(m.in_features == f.in_features and m._cb == f._cb for m in members)
                 and all(m.out_features % 128 == 0 and "bias" not in m for m in members))
 
     @property

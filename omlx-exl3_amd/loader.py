@@ -131,8 +131,9 @@ def load_exl3_tensors(model: nn.Module, model_path, sanitize_key: Callable[[str]
 
 
 def group_siblings(model: nn.Module) -> int:
-    """Group same-input EXL3 siblings (q/k/v, gate/up, in_proj_qkv/z) into single-launch groups,
-    partitioned by (K, codebook) since one launch needs one bitrate (loader.py:137-156)."""
+    """Group same-input EXL3 siblings (q/k/v, gate/up, in_proj_qkv/z) into single-launch groups, partitioned
+    by codebook (loader.py:137-156 partitions by (K, codebook); here one launch also serves members of
+    different K)."""
     groups = 0
     for _, module in model.named_modules():
         for names in SIBLINGS:
@@ -143,7 +144,7 @@ def group_siblings(model: nn.Module) -> int:
                 m._prepare()
             by_rate: dict = {}
             for m in members:
-                by_rate.setdefault((m._K, m._cb), []).append(m)
+                by_rate.setdefault(m._cb, []).append(m)
             for subset in by_rate.values():
                 if EXL3SiblingGroup.fusable(subset):
                     EXL3SiblingGroup(subset)

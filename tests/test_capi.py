@@ -147,6 +147,27 @@ def test_overlapping_outputs_are_rejected(capi):
     assert fused(4, x, None, None, None, None, None) == -1 and "prologue" in _err(capi)
 
 
+def test_gemv_fused_mk_argument_errors(capi):
+    """The mixed-width entry point checks each member's K and refuses the one-K layouts when widths differ
+    (host-side checks, before any launch; the pointers are never dereferenced)."""
+    lib = capi.lib()
+    xh, svh, y = (ctypes.c_void_p(0x100000 + i * 0x10000) for i in range(3))
+    trs = (ctypes.c_void_p * 3)(0x200000, 0x300000, 0x200000)
+    ns = (ctypes.c_int * 3)(128, 128, 0)
+
+    def mk(Ks, flags=0):
+        kk = None if Ks is None else (ctypes.c_int * 3)(*(list(Ks) + [0] * (3 - len(Ks))))
+        return lib.exl3_gemv_fused_mk(0, xh, None, None, None, None, 0.0, None, None, trs, 2, ns, kk, 256, 0, svh,
+                                      None, y, 0, 1, flags, None, None, None, 0, None)
+
+    assert mk(None) == -1 and "member_K" in _err(capi)
+    assert mk((4, 9)) == -1 and "K must be 1..8" in _err(capi)
+    assert mk((0, 4)) == -1 and "K must be 1..8" in _err(capi)
+    assert mk((4, 6), flags=1) == -1 and "exact layout" in _err(capi)     # EXL3_GEMV_FAST
+    assert mk((4, 6), flags=2) == -1 and "exact layout" in _err(capi)     # EXL3_GEMV_TABLE
+    assert mk((4, 6)) == -2                                                # passes the K checks: no workspace
+
+
 def test_library_has_no_unresolved_own_symbols(capi):
     """Every exl3 symbol the library uses is defined in it (a kernel whose host stub the compiler did not emit
     would otherwise surface only when the library is loaded on a GPU box)."""

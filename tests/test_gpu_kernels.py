@@ -6,6 +6,7 @@ fp64 reference, the reference's own bars (exl3_kernel_test.py:50). Full 27B-clas
 through size-independent properties: GEMV == (bit-exact reconstruct, fp32 matmul, Hadamard, svh);
 bitwise determinism; row-exactness (row r identical for any row count).
 """
+import ctypes
 import math
 
 import numpy as np
@@ -248,6 +249,69 @@ def test_gemv_27b_shapes_mixed_bitrates(pk, name, K, rows):
     assert e < 2e-3, (name, K, rows, e)
     y1 = pk.kernels.TrellisGemvPlan(k, ns, K, 0, svh, 1, torch.float32)(xh[:, :1].contiguous(), trs)
     assert torch.equal(y1[0], y[0])
+
+
+@pytest.mark.parametrize("name,Ks,rows,cb,odt", [
+    ("qkv", (6, 4, 4), 1, 0, torch.float32), ("qkv", (2, 8, 5), 4, 0, torch.float16),
+    ("gate_up", (4, 6), 1, 0, torch.float32), ("gate_up", (3, 8), 8, 1, torch.bfloat16),
+    ("kv", (7, 1), 2, 2, torch.float32), ("qkv", (5, 3, 6), 16, 1, torch.float32)])
+def test_gemv_members_of_different_bitrates(pk, name, Ks, rows, cb, odt):
+    """Siblings of different K in one launch (the mixed-width kernel): against had128(xh @ W) * svh per member
+    with W from the bit-exact reconstruct kernel and an fp32 matmul; deterministic; row 0 equals the
+    single-row launch bit for bit; members of one K through the same entry point equal exl3_gemv_fused."""
+    k, ns = SHAPES_27B[name]
+    g = torch.Generator(device="cuda").manual_seed(sum(Ks) * 31 + rows)
+    trs = [torch.randint(-32768, 32768, (k // 16, n // 16, 16 * K), dtype=torch.int16, device="cuda", generator=g)
+           for n, K in zip(ns, Ks)]
+    svh = (torch.randn(sum(ns), device="cuda", generator=g) * 0.01).half()
+    xh = torch.randn((len(ns), rows, k), device="cuda", generator=g).half()
+    Ws = [pk.kernels.decode_wt(t, k, n, K, cb).float() for t, n, K in zip(trs, ns, Ks)]
+    ref = torch.cat([_had128_t(xh[m].float() @ Ws[m].T) for m in range(len(ns))], dim=1) * svh.float()
+    plan = pk.kernels.TrellisGemvPlan(k, ns, Ks, cb, svh, rows, odt)
+    assert plan.mixed
+    y = plan(xh, trs)
+    e = ((y.float() - ref).abs().max() / ref.abs().max()).item()
+    tol = 1e-2 if odt == torch.bfloat16 else 2e-3
+    assert e < tol, (name, Ks, rows, e)
+    assert torch.equal(y, plan(xh, trs))                                   # deterministic
+    y1 = pk.kernels.TrellisGemvPlan(k, ns, Ks, cb, svh, 1, odt)(xh[:, :1].contiguous(), trs)
+    assert torch.equal(y1[0], y[0])                                        # row-exact
+    # one K through the mixed-width entry point is exl3_gemv_fused with that K, bit for bit
+    K0 = Ks[0]
+    trs0 = [torch.randint(-32768, 32768, (k // 16, n // 16, 16 * K0), dtype=torch.int16, device="cuda",
+                          generator=g) for n in ns]
+    p_one = pk.kernels.TrellisGemvPlan(k, ns, K0, cb, svh, rows, odt)
+    out_mk = torch.empty_like(y)
+    lib = pk._capi.lib()
+    Kc = (ctypes.c_int * 3)(*([K0] * 3))
+    p_one._bind(trs0, None, out_mk, xh.device)
+    rc = lib.exl3_gemv_fused_mk(0, xh.data_ptr(), None, None, None, None, 0.0, None, None, p_one._tr_c, p_one.nsub,
+                                p_one._ns_c, Kc, k, cb, p_one.svh.data_ptr(), None, out_mk.data_ptr(),
+                                pk.kernels.DTYPE_CODE[odt], rows, 0, None, None, p_one.workspace.data_ptr(),
+                                p_one.workspace.numel(), pk.kernels.stream_handle(xh.device))
+    assert rc == 0
+    assert torch.equal(out_mk, p_one.fused(pk.kernels.PROLOGUE_NONE, xh, trs0))
+
+
+def test_gemv_different_bitrates_with_norm_prologue(pk):
+    """The mixed-width launch with the RMSNorm prologue and the residual / block-sum epilogue equals the
+    rotation kernels followed by the plain mixed-width launch, bit for bit (the 27B q/k/v group at K 6, 4, 4)."""
+    k, ns, Ks = 5120, [6144, 1024, 1024], (6, 4, 4)
+    g = torch.Generator(device="cuda").manual_seed(11)
+    trs = [torch.randint(-32768, 32768, (k // 16, n // 16, 16 * K), dtype=torch.int16, device="cuda", generator=g)
+           for n, K in zip(ns, Ks)]
+    svh = torch.where(torch.rand(sum(ns), device="cuda", generator=g) < 0.5, -1.0, 1.0).half()
+    suh = torch.where(torch.rand((3, k), device="cuda", generator=g) < 0.5, -1.0, 1.0).half()
+    x = torch.randn((1, k), device="cuda", generator=g).half()
+    res = torch.randn((1, k), device="cuda", generator=g).half()
+    w = (1.0 + 0.1 * torch.randn(k, device="cuda", generator=g)).half()
+    plan = pk.kernels.TrellisGemvPlan(k, ns, Ks, 0, svh, 1, torch.float16)
+    h_out = torch.empty_like(x)
+    y_f = plan.rmsnorm(x, res, w, 1e-6, suh, trs, residual_out=h_out)
+    _xn, xh, h = pk.kernels.norm_rot(x, w, 1e-6, suh, residual=res)
+    y_u = plan(xh.contiguous(), trs)
+    assert torch.equal(y_f, y_u)
+    assert torch.equal(h_out, h)
 
 
 def test_gemv_bias_and_split_override(pk):

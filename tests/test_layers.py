@@ -14,7 +14,7 @@ from conftest import load_package
 from oracle import exl3_oracle as O
 
 pk = load_package()
-from omlx_exl3_amd import fusion, linear, loader, synthetic  # noqa: E402
+from omlx_exl3_amd import fusion, kernels, linear, loader, synthetic  # noqa: E402
 
 
 def _parts(k, n, K, legacy=False, cb=0, bias=False):
@@ -103,11 +103,30 @@ def test_sibling_fusable_rules():
     mk = lambda n, K=6, cb=0, bias=False: linear.EXL3Linear(256, n, _parts(256, n, K, cb=cb, bias=bias))  # noqa: E731
     assert linear.EXL3SiblingGroup.fusable([mk(256), mk(128)])
     assert not linear.EXL3SiblingGroup.fusable([mk(256)])                       # one member
-    assert not linear.EXL3SiblingGroup.fusable([mk(256), mk(128, K=4)])         # bitrates differ
+    assert linear.EXL3SiblingGroup.fusable([mk(256), mk(128, K=4)])             # bitrates may differ
+    assert linear.EXL3SiblingGroup.fusable([mk(256, K=2), mk(128, K=8), mk(128, K=5)])
     assert not linear.EXL3SiblingGroup.fusable([mk(256), mk(128, cb=1)])        # codebooks differ
     assert not linear.EXL3SiblingGroup.fusable([mk(256), mk(144)])              # n % 128
     assert not linear.EXL3SiblingGroup.fusable([mk(256), mk(128, bias=True)])   # bias
     assert not linear.EXL3SiblingGroup.fusable([mk(128)] * 4)                   # > 3 members
+    g = linear.EXL3SiblingGroup([mk(256, K=3), mk(128, K=6)])
+    assert g.Ks == [3, 6] and g.K == (3, 6)
+
+
+def test_gemv_plan_member_bitrates():
+    """A plan over members of different K checks each member's trellis at its own K and refuses the layouts
+    that only one-K launches have (fast, table, an explicit split)."""
+    svh = torch.ones(256, dtype=torch.float16)
+    with pytest.raises(ValueError):
+        kernels.TrellisGemvPlan(256, [128, 128], (4, 6), 0, svh, 1, fast=True)
+    with pytest.raises(ValueError):
+        kernels.TrellisGemvPlan(256, [128, 128], (4, 6), 0, svh, 1, table=True)
+    with pytest.raises(ValueError):
+        kernels.TrellisGemvPlan(256, [128, 128], (4, 6), 0, svh, 1, kt_per_split=8)
+    with pytest.raises(ValueError):
+        kernels.TrellisGemvPlan(256, [128, 128], (4, 9), 0, svh, 1)
+    with pytest.raises(ValueError):
+        kernels.TrellisGemvPlan(256, [128, 128], (4,), 0, svh, 1)
 
 
 # ------------------------------------------------------------------------------------------ loader
@@ -212,10 +231,12 @@ def test_load_swaps_loads_groups_and_fuses(tmp_path):
     _write_checkpoint(tmp_path, ts)
     info = loader.load_exl3(m, tmp_path)
     assert info["linears"] == 15 and info["tensors"] == sum(1 for k in ts if not k.startswith("model.norm"))
-    # q at K=6 stays alone, k/v at K=4 form a group; gate/up form a group (loader.py:137-156)
+    # q at K=6 and k/v at K=4 form one group (the reference, loader.py:137-156, would leave q alone: one launch
+    # serves members of different K here); gate/up form a group
     assert info["groups"] == 4
     att = m.model.layers[0].self_attn
-    assert att.q_proj._group is None and att.k_proj._group is att.v_proj._group is not None
+    assert att.q_proj._group is att.k_proj._group is att.v_proj._group is not None
+    assert att.q_proj._group.Ks == [6, 4, 4]
     assert isinstance(m.model.layers[0].mlp.gate_proj._group, linear.EXL3SiblingGroup)
     assert info["fused"] == {"layer": 2, "norm": 5, "mlp": 2, "head": 1}
     step = m.model.layers[0].__dict__["forward"]
@@ -225,8 +246,8 @@ def test_load_swaps_loads_groups_and_fuses(tmp_path):
     down = m.model.layers[1].mlp.down_proj
     assert torch.equal(down.sv, ts["model.layers.1.mlp.down_proj.sv"]) and down.K == 6
     assert np.array_equal(down._svh.numpy(), O.unpack_signs(ts["model.layers.1.mlp.down_proj.sv"].numpy()))
-    # the norm feeding q (alone) and k/v (group): two consumer launches, q first
-    assert step.in_consumers == [att.q_proj, att.k_proj._group] and step.out_proj is att.o_proj
+    # the norm feeds one consumer launch: the q/k/v group of mixed K
+    assert step.in_consumers == [att.q_proj._group] and step.out_proj is att.o_proj
     assert step.gate_up is m.model.layers[0].mlp.gate_proj._group and step.down is m.model.layers[0].mlp.down_proj
     assert isinstance(m.model.norm.__dict__["forward"], fusion.HeadNorm)
     assert fusion.unfuse(m) == 3 and "forward" not in m.model.layers[0].__dict__
