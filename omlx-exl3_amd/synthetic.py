@@ -51,13 +51,19 @@ class DecoderConfig:
     codebook: int = 0
     rope_theta: float = 1_000_000.0
     max_len: int = 1024
+    K_by_proj: dict | None = None   # bits per weight of single projections ("q_proj", ..., "lm_head"), else K
+
+    def k_of(self, proj: str) -> int:
+        return (self.K_by_proj or {}).get(proj, self.K)
 
     def layer_trellis_bytes(self) -> int:
         h, q, kv, m = self.hidden, self.n_heads * self.head_dim, self.n_kv_heads * self.head_dim, self.intermediate
-        return self.K * (h * (q + 2 * kv) + q * h + 2 * h * m + m * h) // 8
+        sizes = {"q_proj": h * q, "k_proj": h * kv, "v_proj": h * kv, "o_proj": q * h, "gate_proj": h * m,
+                 "up_proj": h * m, "down_proj": m * h}
+        return sum(self.k_of(p) * w for p, w in sizes.items()) // 8
 
     def head_trellis_bytes(self) -> int:
-        return self.K * self.hidden * self.vocab // 8
+        return self.k_of("lm_head") * self.hidden * self.vocab // 8
 
 
 def random_exl3_linear(k: int, n: int, K: int, cb: int, gen: torch.Generator, device, bias: bool = False,
@@ -115,10 +121,10 @@ class Attention(nn.Module):
         super().__init__()
         h, q, kv = cfg.hidden, cfg.n_heads * cfg.head_dim, cfg.n_kv_heads * cfg.head_dim
         self.cfg = cfg
-        self.q_proj = random_exl3_linear(h, q, cfg.K, cfg.codebook, gen, device)
-        self.k_proj = random_exl3_linear(h, kv, cfg.K, cfg.codebook, gen, device)
-        self.v_proj = random_exl3_linear(h, kv, cfg.K, cfg.codebook, gen, device)
-        self.o_proj = random_exl3_linear(q, h, cfg.K, cfg.codebook, gen, device)
+        self.q_proj = random_exl3_linear(h, q, cfg.k_of("q_proj"), cfg.codebook, gen, device)
+        self.k_proj = random_exl3_linear(h, kv, cfg.k_of("k_proj"), cfg.codebook, gen, device)
+        self.v_proj = random_exl3_linear(h, kv, cfg.k_of("v_proj"), cfg.codebook, gen, device)
+        self.o_proj = random_exl3_linear(q, h, cfg.k_of("o_proj"), cfg.codebook, gen, device)
         self.fused_attn = True
         self.register_buffer("k_cache", torch.zeros(cfg.n_kv_heads, cfg.max_len, cfg.head_dim,
                                                     dtype=torch.float16, device=device), persistent=False)
@@ -171,9 +177,9 @@ class MLP(nn.Module):
     def __init__(self, cfg: DecoderConfig, gen, device):
         super().__init__()
         h, m = cfg.hidden, cfg.intermediate
-        self.gate_proj = random_exl3_linear(h, m, cfg.K, cfg.codebook, gen, device)
-        self.up_proj = random_exl3_linear(h, m, cfg.K, cfg.codebook, gen, device)
-        self.down_proj = random_exl3_linear(m, h, cfg.K, cfg.codebook, gen, device)
+        self.gate_proj = random_exl3_linear(h, m, cfg.k_of("gate_proj"), cfg.codebook, gen, device)
+        self.up_proj = random_exl3_linear(h, m, cfg.k_of("up_proj"), cfg.codebook, gen, device)
+        self.down_proj = random_exl3_linear(m, h, cfg.k_of("down_proj"), cfg.codebook, gen, device)
 
     def forward(self, x):
         return self.down_proj(F.silu(self.gate_proj(x)) * self.up_proj(x))
@@ -210,7 +216,7 @@ class SyntheticDecoder(nn.Module):
                 torch.randn(cfg.vocab, cfg.hidden, generator=gen, device=device, dtype=torch.float32).half())
         self.model.layers = nn.ModuleList([DecoderLayer(cfg, gen, device) for _ in range(cfg.n_layers)])
         self.model.norm = nn.RMSNorm(cfg.hidden, eps=cfg.eps, device=device, dtype=torch.float16)
-        self.lm_head = random_exl3_linear(cfg.hidden, cfg.vocab, cfg.K, cfg.codebook, gen, device)
+        self.lm_head = random_exl3_linear(cfg.hidden, cfg.vocab, cfg.k_of("lm_head"), cfg.codebook, gen, device)
         cos, sin = _rope_tables(cfg, device)
         self.register_buffer("rope_cos", cos, persistent=False)
         self.register_buffer("rope_sin", sin, persistent=False)

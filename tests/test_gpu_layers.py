@@ -145,10 +145,13 @@ def test_synthetic_decode_forms_and_their_launches(pk):
             t.copy_(toks[0])                                   # keep all on the same token stream
 
 
-def test_decoder_graph_replay_matches_eager(pk):
+@pytest.mark.parametrize("mixed", [False, True], ids=["K6", "mixedK"])
+def test_decoder_graph_replay_matches_eager(pk, mixed):
     from omlx_exl3_amd.synthetic import SyntheticDecoder, greedy_step
 
     cfg = _tiny_cfg()
+    if mixed:
+        cfg.K_by_proj = {"q_proj": 2, "k_proj": 5, "v_proj": 4, "gate_proj": 8, "up_proj": 3, "lm_head": 5}
     eager = SyntheticDecoder(cfg, seed=5, device="cuda")
     graphed = SyntheticDecoder(cfg, seed=5, device="cuda")
     ids = torch.randint(0, cfg.vocab, (16,), device="cuda", generator=torch.Generator(device="cuda").manual_seed(6))
@@ -178,22 +181,26 @@ def test_decoder_graph_replay_matches_eager(pk):
         _ = (torch.randn(4096, device="cuda") * 2).sum().item()      # unrelated eager work between replays
 
 
-def test_loader_end_to_end_on_gpu(pk, tmp_path):
+@pytest.mark.parametrize("Ks", [(5, 5, 5), (6, 3, 8)])
+def test_loader_end_to_end_on_gpu(pk, tmp_path, Ks):
+    """A checkpoint of q/k/v at the given bitrates through load_exl3: one sibling group (one launch at decode
+    rows, also when the members' K differ), each member within 2e-3 of the oracle."""
     from safetensors.torch import save_file
     from torch import nn
     from omlx_exl3_amd import loader
 
-    k, nq, nkv, K = 512, 512, 256, 5
+    k, nq, nkv = 512, 512, 256
     tensors, refs = {}, {}
     rng = np.random.default_rng(9)
     for i, (name, n) in enumerate((("q_proj", nq), ("k_proj", nkv), ("v_proj", nkv))):
+        K = Ks[i]
         tr = O.random_trellis(k, n, K, 40 + i)
         suh = np.where(rng.integers(0, 2, k) == 1, 1.0, -1.0).astype(np.float16)
         svh = (rng.standard_normal(n) / math.sqrt(k)).astype(np.float16)
         p = f"layers.0.self_attn.{name}"
         tensors[f"{p}.trellis"] = torch.from_numpy(np.ascontiguousarray(tr).view(np.int16))
         tensors[f"{p}.suh"], tensors[f"{p}.svh"] = torch.from_numpy(suh), torch.from_numpy(svh)
-        refs[name] = (tr, n, suh, svh)
+        refs[name] = (tr, n, K, suh, svh)
     save_file(tensors, str(tmp_path / "model.safetensors"))
 
     class Attn(nn.Module):
@@ -214,12 +221,15 @@ def test_loader_end_to_end_on_gpu(pk, tmp_path):
     info = loader.load_exl3(model, tmp_path)
     assert info["linears"] == 3 and info["groups"] == 1
     att = model.layers[0].self_attn
+    assert att.q_proj._group is att.k_proj._group is att.v_proj._group is not None
     x = torch.randn(2, k, device="cuda").half()
+    with LibCalls() as calls:
+        ys = {name: getattr(att, name)(x) for name in ("q_proj", "k_proj", "v_proj")}
+    assert calls.total() == 1, calls.counts                 # the rotation inside the one GEMV launch
     for name in ("q_proj", "k_proj", "v_proj"):
-        tr, n, suh, svh = refs[name]
-        y = getattr(att, name)(x)
+        tr, n, K, suh, svh = refs[name]
         ref = O.linear_ref(x.float().cpu().numpy(), tr, k, n, K, 0, suh, svh)
-        assert O.max_abs_rel(y.float().cpu().numpy(), ref) < 2e-3, name
+        assert O.max_abs_rel(ys[name].float().cpu().numpy(), ref) < 2e-3, name
 
 
 def test_decoder_matches_fp32_reference_built_from_reconstructed_weights(pk):

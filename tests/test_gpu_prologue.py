@@ -89,13 +89,24 @@ def test_gemv_prologue_rejects_bad_arguments(pk):
                    torch.ones(1, 1040, dtype=torch.float16, device="cuda"), _trellises(1040, ns, K, 32))
 
 
-def test_decoder_gemv_prologues_match_layer_by_layer(pk):
+MIXED_K = {"q_proj": 6, "k_proj": 3, "v_proj": 8, "o_proj": 4, "gate_proj": 5, "up_proj": 2, "down_proj": 8,
+           "lm_head": 4}
+
+
+@pytest.mark.parametrize("kmap", [None, MIXED_K], ids=["K6", "mixedK"])
+def test_decoder_gemv_prologues_match_layer_by_layer(pk, kmap):
+    """The five-launch decode step (norms, SwiGLU and residual adds inside the GEMV launches) equals the
+    layer-by-layer step bit for bit, also with every projection at its own bitrate (q/k/v and gate/up then
+    run as mixed-width launches)."""
     from omlx_exl3_amd.synthetic import DecoderConfig, SyntheticDecoder, greedy_step
 
     cfg = DecoderConfig(n_layers=3, hidden=512, intermediate=1024, n_heads=4, n_kv_heads=2, head_dim=128,
-                        vocab=2048, max_len=64)
+                        vocab=2048, max_len=64, K_by_proj=kmap)
     deep = SyntheticDecoder(cfg, seed=8, device="cuda")
     layered = SyntheticDecoder(cfg, seed=8, device="cuda", gemv_prologues=False)
+    if kmap:
+        att = deep.model.layers[0].self_attn
+        assert att.q_proj._group is not None and att.q_proj._group.Ks == [6, 3, 8]
     ids = torch.randint(0, cfg.vocab, (10,), device="cuda", generator=torch.Generator(device="cuda").manual_seed(9))
     pos = torch.arange(10, device="cuda")
     assert torch.equal(deep(ids, pos), layered(ids, pos))                         # prefill: same path
