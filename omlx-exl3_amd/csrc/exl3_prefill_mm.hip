@@ -149,8 +149,9 @@ __global__ __launch_bounds__(kMmThreads) __attribute__((amdgpu_waves_per_eu(2)))
   // first, one tile load of step s + 2 into half s & 1; then the MFMAs of slice 0 of step s + 1 with the reads of
   // its slice 1. The order is fixed instruction by instruction (sched_barrier(0) after each group): left to
   // itself the scheduler issues a pass's tile loads back to back, and the wavefronts, all leaving the barrier
-  // together, then wait on the load path instead of feeding the MFMA pipe (one load per three MFMAs measured 6%
-  // faster on gate/up at 4,608 rows than that burst, one per two 2% slower than one per three; the same on down).
+  // together, then wait on the load path instead of feeding the MFMA pipe (at 4,608 rows, one load per three
+  // MFMAs measured 6% faster on gate/up than that burst and 2% faster than one per two; on down all three
+  // orders were within 1%).
   u32x4 fa0[TI], fb0[8], fa1[TI], fb1[8];
   auto read_slice = [&](int buf, int h, u32x4 (&fa)[TI], u32x4 (&fb)[8]) {
 #pragma unroll
