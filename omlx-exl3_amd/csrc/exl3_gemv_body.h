@@ -20,7 +20,8 @@ template <bool SPLIT>
 __device__ void stage_prologue(const GemvArgs& a, int m, int blk_in_member, int kt0, int kt1, int nrec, u32x4* xs,
                                double (*ss_part)[16], float* inv_rms) {
   constexpr int RW = SPLIT ? 4 : 2;
-  const int tid = threadIdx.x, nthr = blockDim.x, lane = tid & 63, wave = tid >> 6, nw = nthr >> 6;
+  const int tid = threadIdx.x, nthr = blockDim.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6),
+            nw = nthr >> 6;
   const int rows = a.rows, k = a.k, nkt = kt1 - kt0;
   // zero records: k-tiles past the split (read by the look-ahead) and the absent-row record
   for (int idx = nkt * rows * RW + tid; idx < (nrec + 1) * RW; idx += nthr) xs[idx] = u32x4{0u, 0u, 0u, 0u};
@@ -164,7 +165,8 @@ template <bool SPLIT>
 __device__ void prologue_finish(const GemvArgs& a, const ProPre& p, int kt0, int kt1, int nrec, u32x4* xs,
                                 double (*ss_part)[16], float* inv_rms, bool write_xn) {
   constexpr int RW = SPLIT ? 4 : 2;
-  const int tid = threadIdx.x, nthr = blockDim.x, lane = tid & 63, wave = tid >> 6, nw = nthr >> 6;
+  const int tid = threadIdx.x, nthr = blockDim.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6),
+            nw = nthr >> 6;
   const int nkt = kt1 - kt0;
   for (int idx = nkt * RW + tid; idx < (nrec + 1) * RW; idx += nthr) xs[idx] = u32x4{0u, 0u, 0u, 0u};
   if (a.pro == kProNorm) {
@@ -236,7 +238,9 @@ __device__ __forceinline__ void gemv_body(const GemvArgs a, u32x4* xs, float (*b
   // 256 x WK threads: wavefront w serves column group cw = w % 4 (two n-tiles) and k-group kg = w / 4, which
   // takes the split's iterations kg, kg + WK, kg + 2 WK, ...; the k-groups' sums are added in LDS in k-group
   // order. More k-groups put more wavefronts on each SIMD for narrow outputs without adding split-K traffic.
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  // (wave through readfirstlane: the compiler then keeps the wavefront-uniform values derived from it, k-group,
+  // column group, iteration counts, in scalar registers instead of spending VALU instructions on them)
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int nthr = blockDim.x, WK = nthr >> 8;
   const int cw = wave & 3, kg = wave >> 2;
   const int blk = blockIdx.x, s = blockIdx.y;
@@ -249,7 +253,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs a, u32x4* xs, float (*b
   const int kt1 = min(a.KT, kt0 + a.kt_per_split);
   const int nkt = kt1 - kt0;
   const int iters = (nkt + 3) >> 2;
-  const int my_iters = iters > kg ? (iters - kg + WK - 1) / WK : 0;   // this k-group's iterations
+  const int my_iters = iters > kg ? (iters - kg + WK - 1) >> (WK - 1) : 0;   // this k-group's iterations (WK 1 or 2)
 
   const int q = lane >> 4, c = lane & 15, g = c & 7;
   const int nt_local = (blk - blk0) * 8 + cw * 2 + (c >> 3);
