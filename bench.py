@@ -276,19 +276,51 @@ def mixed_k_benchmark(pk, torch, dev, rows_list=(1, 2, 4, 8), n_layers=8, reps=1
     return out
 
 
+# PyTorch TunableOp's table of the fastest hipBLASLt / rocBLAS solution of each 27B projection GEMM at 16..4608
+# rows on MI355X (hipBLASLt's default heuristic does not pick it for these shapes); read by the platform-BLAS
+# comparison leg of the prefill measurement only.
+GEMM_TABLE = os.path.join(ROOT, "bench_gemm_table_mi355x.csv")
+
+
+def blas_prefill(pk, torch, xh, tr, k, n, K, cb, svh, out, table_ok):
+    """The reference's prefill structure on the platform BLAS, for comparison only (linear.py:97-105):
+    reconstruct W_inner^T (exl3_reconstruct), an fp16 GEMM with fp32 accumulation by hipBLASLt through
+    torch.matmul (TunableOp on with tuning off around the call, so a shape GEMM_TABLE lists runs its recorded
+    solution), then the output rotation (exl3_prefill_out_rotate)."""
+    wt = pk.kernels.decode_wt(tr, k, n, K, cb)
+    if table_ok:
+        tun = torch.cuda.tunable
+        was_on, was_tuning = tun.is_enabled(), tun.tuning_is_enabled()
+        tun.tuning_enable(False)
+        tun.enable(True)
+        try:
+            g = torch.matmul(xh, wt.t())
+        finally:
+            tun.enable(was_on)
+            tun.tuning_enable(was_tuning)
+    else:
+        g = torch.matmul(xh, wt.t())
+    return pk.kernels.prefill_out_rotate(g, svh, None, out)
+
+
 def prefill_benchmark(pk, torch, dev, rows=4608, reps=6) -> dict:
     """Config 4: M = 4608 rotated fp16 activations through gate / up (5120 -> 17408) and down (17408 -> 5120)
-    at K = 6. Three prefill forms are timed: "matmul" (W_inner^T reconstructed once, then the hand-written MFMA
-    GEMM with the output rotation in its epilogue), "fused" (trellis tiles reconstructed in LDS, MFMA, Hadamard
-    epilogue, one launch) and "library" (reconstruct, hipBLASLt fp16 GEMM with the tabled solution, output
-    rotation: the reference's structure on the platform BLAS, for comparison); the headline figures are those
-    of the form prefill_gemm picks at this row count ("auto"). Every form first runs twice over the three
+    at K = 6. Forms timed: "matmul" (W_inner^T reconstructed, then the hand-written MFMA GEMM with the output
+    rotation in its epilogue: prefill_gemm's default), "fused" (trellis tiles reconstructed in LDS, MFMA, Hadamard
+    epilogue, one launch), and for comparison "blas" (reconstruct, hipBLASLt fp16 GEMM with the tabled solution,
+    output rotation: the reference's structure on the platform BLAS). Every form first runs twice over the three
     projections (warm clocks, allocator, plans); a form's figure is then the GPU time of `reps` back-to-back
     passes over gate, up and down (HIP events, the region starting behind one more untimed pass so the GPU is
     busy when it opens); per projection the same with that projection alone. TFLOP/s = 2 M k n / time,
     against the 2.5 PFLOP/s dense fp16 MFMA peak."""
     g = torch.Generator(device=dev).manual_seed(5)
-    paths = ("matmul", "fused", "library")
+    table_ok = False
+    if os.path.exists(GEMM_TABLE):
+        try:
+            table_ok = bool(torch.cuda.tunable.read_file(GEMM_TABLE))   # False if its version lines differ
+        except RuntimeError:
+            table_ok = False
+    paths = ("matmul", "fused", "blas")
     shapes = (("gate", 5120, 17408), ("up", 5120, 17408), ("down", 17408, 5120))
     data = {}
     for name, k, n in shapes:
@@ -300,7 +332,10 @@ def prefill_benchmark(pk, torch, dev, rows=4608, reps=6) -> dict:
 
     def call(name, path):
         k, n, tr, svh, xh, out = data[name]
-        pk.kernels.prefill_gemm(xh, tr, k, n, 6, 0, svh, out=out, path=path)
+        if path == "blas":
+            blas_prefill(pk, torch, xh, tr, k, n, 6, 0, svh, out, table_ok)
+        else:
+            pk.kernels.prefill_gemm(xh, tr, k, n, 6, 0, svh, out=out, path=path)
 
     def timed(names, path):
         for nm in names:   # left running while the timed calls are queued
@@ -333,7 +368,7 @@ def prefill_benchmark(pk, torch, dev, rows=4608, reps=6) -> dict:
     tf = {p: tot[p][0] / tot[p][1] / 1e9 for p in tot}
     return {"rows": rows, "path": auto, "per_proj": per[auto], "TFLOP_s": round(tf[auto], 1),
             "peak_TFLOP_s": MFMA_F16_PEAK_TFLOPS, "mfma_frac": round(tf[auto] / MFMA_F16_PEAK_TFLOPS, 4),
-            "ms_total": round(tot[auto][1], 2), "gemm_table": pk.kernels._gemm_table_loaded(),
+            "ms_total": round(tot[auto][1], 2), "blas_gemm_table": table_ok,
             "by_path": {p: {"TFLOP_s": round(tf[p], 1), "ms_total": round(tot[p][1], 2), "per_proj": per[p]}
                         for p in per}}
 
@@ -395,7 +430,8 @@ def decode_benchmark(pk, torch, dev, n_layers: int, prompt: int, gen: int) -> di
             "prompt": prompt, "gen_tokens": gen, "bytes_per_token": int(bpt),
             "GB_s": round(bpt * tok_s / 1e9, 1), "pct_hbm_peak": round(100 * bpt * tok_s / 1e9 / HBM_PEAK_GBS, 1),
             "prefill_tok_s": round(prompt / t_prefill, 1), "build_s": round(t_build, 1),
-            "logits_finite": finite, "fused": model.fused, "sibling_groups": model.groups}
+            "logits_finite": finite, "fused": model.fused, "sibling_groups": model.groups,
+            "decode_path": "fusion.fuse_decode: DecodeStep + HeadNorm, prologue form (five launches per layer)"}
 
 
 def main() -> int:

@@ -89,7 +89,8 @@ size_t exl3_gemv_workspace_bytes(int k, int n_total, int rows, int K);
  *   y        (rows, n_total) in out_dtype (EXL3_DTYPE_F16 / BF16 / F32)
  *   rows     1..EXL3_MAX_GEMV_ROWS; flags: EXL3_GEMV_EXACT or EXL3_GEMV_FAST
  * Split-K partials are reduced in a fixed order: results are bitwise reproducible run to run, and
- * row r of the output does not depend on the row count. */
+ * row r of the output does not depend on the row count. y is written while other workgroups still read the
+ * inputs, so it must not overlap xh, svh, bias or a trellis (EXL3_ERR_ARG otherwise; not in place). */
 int exl3_gemv(const uint16_t* xh, const uint32_t* const* trellis, int n_members, const int* member_n,
               int k, int K, int cb, const uint16_t* svh, const void* bias, void* y, int out_dtype, int rows,
               unsigned flags, void* workspace, size_t workspace_bytes, void* stream);
@@ -111,7 +112,8 @@ int exl3_gemv_ex(const uint16_t* xh, const uint32_t* const* trellis, int n_membe
  * allocates and frees nothing (neither here nor in any library routine it calls). The counters keep a fixed
  * 512 KiB region at the array's start (up to 262,144 output columns), so calls of different shapes follow each
  * other safely; a shape whose partials do not fit in the rest is rejected with EXL3_ERR_WORKSPACE (every
- * 27B-class projection fits at up to 8 rows). The first call on a GPU also enqueues one small fill kernel on `stream`
+ * 27B-class decoder projection fits at up to 8 rows; the 5120 -> 151936 output head, whose 7 splits need
+ * 7 x rows x 151936 fp32 partials, only at 1 row). The first call on a GPU also enqueues one small fill kernel on `stream`
  * that zeroes the counter region; every call leaves the counters at zero.
  * All calls on one GPU share its array: calls that can overlap on that GPU (other streams, other host
  * threads without ordering) race and give wrong results; order them on one stream.
@@ -145,7 +147,9 @@ int exl3_gemv_noalloc(const uint16_t* xh, const uint32_t* const* trellis, int n_
  *   suh fp16 (n_members, k); k % 128 == 0 with a prologue.
  * Epilogue (fp16 output only): y = fp16(y + y_residual) when y_residual (rows, n_total) is given (the next
  * norm's residual add; y_residual may be y's own buffer), and y_sumsq (rows, n_total/128) fp64 receives each
- * 128-column block's sum of squares of y when given. The other arguments as exl3_gemv. */
+ * 128-column block's sum of squares of y when given. y must not overlap x, residual, residual_out, xn_out, w,
+ * x_sumsq, suh, y_sumsq, svh, bias, a trellis, or y_residual unless y_residual is y itself (EXL3_ERR_ARG).
+ * The other arguments as exl3_gemv. */
 #define EXL3_PROLOGUE_NONE 0
 #define EXL3_PROLOGUE_RMSNORM 1
 #define EXL3_PROLOGUE_SWIGLU 2
@@ -206,26 +210,29 @@ int exl3_prefill_gemm(const uint16_t* xh, const uint32_t* trellis, int k, int n,
 /* Prefill contraction on reconstructed weights: y = fp16/bf16/fp32(H128(xh @ W_inner)/sqrt(128) * svh) (+ bias)
  * per 128-column block, by a hand-written MFMA GEMM (fp16 operands, fp32 accumulation) whose epilogue applies the
  * output rotation. With exl3_reconstruct writing W_inner^T first, this is the reference's prefill
- * (linear.py:97-105: decode_wt, matmul, hadamard_transform(y) * svh) with each weight decoded once and no
- * intermediate product in HBM.
- *   xh fp16 (rows, k), 16-byte aligned; w_t fp16 (n, k) = W_inner^T (exl3_reconstruct's output), 16-byte
- *   aligned; svh fp16 [n]; bias NULL or [n] in out_dtype (added after the rounding to out_dtype and rounded
- *   again, as the reference adds its bias to the output-typed product); y (rows, n) in out_dtype, 16-byte
- *   aligned. k % 64 == 0, n % 128 == 0, rows >= 1; each operand below 2 GiB.
+ * (linear.py:97-105: decode_wt per column chunk, matmul, hadamard_transform(y) * svh) with each weight decoded
+ * once and no intermediate product in HBM.
+ *   xh fp16 (rows, k), 16-byte aligned; w_t fp16 (n, k) = W_inner^T (exl3_reconstruct's output, or a window of
+ *   n of its columns), 16-byte aligned; svh fp16 [n]; bias NULL or [n] in out_dtype (added after the rounding to
+ *   out_dtype and rounded again, as the reference adds its bias to the output-typed product); y: rows x n in
+ *   out_dtype with a row stride of ldy elements (ldy >= n; ldy times the element size a multiple of 16 bytes),
+ *   16-byte aligned, so a column chunk of a wider output writes its slice in place.
+ *   k % 64 == 0, n % 128 == 0, rows >= 1; xh and w_t each below 2 GiB.
  *   When the shape's tiles would leave at least half of the GPU's CUs idle (few rows), k is split over several
  *   workgroups per tile and a second launch adds the splits in a fixed order: that needs a 16-byte aligned
  *   workspace of exl3_prefill_matmul_workspace_bytes(rows, k, n) bytes (0 when no split is made: the workspace
  *   may then be NULL); EXL3_ERR_WORKSPACE when it is missing or small. Results are deterministic; the split
- *   depends on the shape only. Allocates nothing. */
+ *   depends on the shape only, so a row's result can differ in the last bits between prefill calls of
+ *   different row counts (the reference's MLX matmul is not row-exact either). Allocates nothing. */
 int exl3_prefill_matmul(const uint16_t* xh, const uint16_t* w_t, int rows, int k, int n, const uint16_t* svh,
-                        const void* bias, void* y, int out_dtype, void* workspace, size_t workspace_bytes,
+                        const void* bias, void* y, int ldy, int out_dtype, void* workspace, size_t workspace_bytes,
                         void* stream);
 
 /* Workspace bytes exl3_prefill_matmul needs for a shape (0: none; also 0 for an invalid shape, which the
  * entry point then rejects). */
 size_t exl3_prefill_matmul_workspace_bytes(int rows, int k, int n);
 
-/* Output rotation for a prefill whose GEMM runs elsewhere (the package's "library" comparison form, built as
+/* Output rotation for a prefill whose GEMM runs elsewhere (bench.py's platform-BLAS comparison, built as
  * the reference's prefill is, linear.py:97-105): exl3_reconstruct writes W_inner^T (bit-exact fp16), the
  * caller multiplies g = xh @ W_inner in fp16 with fp32 accumulation using its BLAS library, and this entry
  * point replaces the reference's hadamard_transform(g) * svh: y = fp16(H128(g)/sqrt(128) * svh) (+ bias) per

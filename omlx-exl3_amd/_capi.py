@@ -39,7 +39,8 @@ _SIGNATURES = {
                                      _vp]),
     "exl3_swiglu_rotate": (_c_int, [_vp, _vp, _c_int, _c_int, _vp, _vp]),
     "exl3_prefill_gemm": (_c_int, [_vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _c_int, _c_int, _vp]),
-    "exl3_prefill_matmul": (_c_int, [_vp, _vp, _c_int, _c_int, _c_int, _vp, _vp, _vp, _c_int, _vp, _c_size, _vp]),
+    "exl3_prefill_matmul": (_c_int, [_vp, _vp, _c_int, _c_int, _c_int, _vp, _vp, _vp, _c_int, _c_int, _vp, _c_size,
+                                     _vp]),
     "exl3_prefill_matmul_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int]),
     "exl3_prefill_out_rotate": (_c_int, [_vp, _c_int, _c_int, _vp, _vp, _vp, _c_int, _vp]),
     "exl3_attn_decode_rotate": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp,

@@ -206,6 +206,25 @@ static int gemv_run(const uint16_t* xh, const GemvPrologueArgs& pro, const uint3
     a.blk_end[i] = 1 << 30;
   }
   const int KT = k / 16, blocks = n_total / 128;
+  {   // y is written while other workgroups still read the inputs: no overlap with any of them (y_residual may be
+      // y itself, each element then read and written by the same lane)
+    const size_t yb = (size_t)rows * n_total * (out_dtype == kF32 ? 4 : 2), rk = (size_t)rows * k * 2;
+    const size_t xb = pro.mode == kProNone ? (size_t)n_members * rk : pro.mode == kProSwiglu ? 2 * rk : rk;
+    const size_t sb = (size_t)(pro.mode == kProSwiglu ? 1 : n_members) * k * 2;
+    bool bad = overlaps(y, yb, pro.mode == kProNone ? static_cast<const void*>(xh) : pro.x, xb) ||
+               overlaps(y, yb, pro.residual, rk) || overlaps(y, yb, pro.residual_out, rk) ||
+               overlaps(y, yb, pro.xn_out, rk) || overlaps(y, yb, pro.w, (size_t)k * 2) ||
+               overlaps(y, yb, pro.suh, sb) || overlaps(y, yb, pro.x_sumsq, (size_t)rows * (k / 128) * 8) ||
+               overlaps(y, yb, pro.y_sumsq, (size_t)rows * (n_total / 128) * 8) ||
+               overlaps(y, yb, svh, (size_t)n_total * 2) ||
+               overlaps(y, yb, bias, (size_t)n_total * (out_dtype == kF32 ? 4 : 2)) ||
+               (pro.y_residual != y && overlaps(y, yb, pro.y_residual, (size_t)rows * n_total * 2));
+    for (int i = 0; i < n_members && !bad; ++i)
+      bad = overlaps(y, yb, trellis[i], (size_t)k * member_n[i] / 8 * (member_K ? member_K[i] : K));
+    EXL3_REQUIRE(!bad, EXL3_ERR_ARG,
+                 "exl3_gemv: y must not overlap an input (xh or x, residual, w, suh, sums of squares, svh, bias, "
+                 "trellis), residual_out, xn_out or y_sumsq; y_residual is either y itself or disjoint from it");
+  }
   hipStream_t st = static_cast<hipStream_t>(stream);
   const size_t creg = counter_region ? counter_region : counters_bytes(blocks);
   EXL3_REQUIRE(creg >= counters_bytes(blocks), EXL3_ERR_ARG,

@@ -69,7 +69,7 @@ __device__ __forceinline__ void mm_tile_of(int b, int tiles_m, int tiles_n, int&
 template <int OT, int TI>
 __global__ __launch_bounds__(kMmThreads) __attribute__((amdgpu_waves_per_eu(2))) void prefill_mm_kernel(
     const uint16_t* __restrict__ xh, const uint16_t* __restrict__ wt, int rows, int k, int n,
-    const uint16_t* __restrict__ svh, const void* __restrict__ bias, void* __restrict__ y, int tiles_m,
+    const uint16_t* __restrict__ svh, const void* __restrict__ bias, void* __restrict__ y, int ldy, int tiles_m,
     int tiles_n, float* __restrict__ partials, int steps_per_split) {
   using Tl = MmTile<TI>;
   // [stage][A slots, B slots]: 128 KiB, sized for TI = 4 whatever TI is (one workgroup per CU in every case; an
@@ -286,7 +286,7 @@ __global__ __launch_bounds__(kMmThreads) __attribute__((amdgpu_waves_per_eu(2)))
       for (int j = 0; j < 8; ++j) {
         if constexpr (OT == kF32) {
           const float o = v[j] * kHadScale * sv[j];
-          if (gr < rows) store_from_f32<OT>(y, (size_t)gr * n + colbase + 16 * j, has_bias ? o + bs[j] : o);
+          if (gr < rows) store_from_f32<OT>(y, (size_t)gr * ldy + colbase + 16 * j, has_bias ? o + bs[j] : o);
         } else {
           // rounded to the output type, then the bias added and rounded again (a select, no branch)
           auto bits = [](float x) { return OT == kF16 ? f32_to_f16(x) : f32_to_bf16(x); };
@@ -304,7 +304,7 @@ __global__ __launch_bounds__(kMmThreads) __attribute__((amdgpu_waves_per_eu(2)))
         const int R = 4 * t + (lane >> 4), kc = lane & 15;
         const u32x4 w = *reinterpret_cast<const u32x4*>(stage + stage_at(R, 8 * kc));
         const int gr = row0 + wr + 16 * i + R;
-        if (gr < rows) *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(y) + (size_t)gr * n + col0 + wc + 8 * kc) = w;
+        if (gr < rows) *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(y) + (size_t)gr * ldy + col0 + wc + 8 * kc) = w;
       }
       // the reads are done before the next row block overwrites the region
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -369,18 +369,21 @@ static size_t mm_workspace_bytes(const MmPlan& p, int rows, int n) {
 }
 
 // Reduction of a split launch: y = epilogue(sum of the S partials in split order) per (row, 128-column block),
-// 16 lanes per block, 8 consecutive columns per lane (the FWHT stage order and rounding of the GEMM epilogue).
+// 16 lanes per block, 8 consecutive columns per lane. The FWHT stages run in the GEMM epilogue's order, but the
+// split sums are added in a different order from the unsplit accumulation, so a row's result depends on whether
+// its prefill call splits k (deterministic for a shape; not row-exact across prefill sizes).
 template <int OT>
 __global__ __launch_bounds__(256) void prefill_mm_reduce_kernel(const float* __restrict__ partials, int S, int rows,
                                                                 int n, int groups, const uint16_t* __restrict__ svh,
-                                                                const void* __restrict__ bias, void* __restrict__ y) {
+                                                                const void* __restrict__ bias, void* __restrict__ y,
+                                                                int ldy) {
   const int grp = blockIdx.x * 16 + (threadIdx.x >> 4);
   if (grp >= groups) return;   // whole 16-lane groups leave together: the transform's shuffles stay inside one
   const int nb = n / 128;
   const int r = grp / nb, b = grp - r * nb;
   const int lane = threadIdx.x & 63;
   const int c0 = b * 128 + 8 * (lane & 15);
-  const size_t o0 = (size_t)r * n + c0, split = (size_t)rows * n;
+  const size_t o0 = (size_t)r * n + c0, split = (size_t)rows * n, oy = (size_t)r * ldy + c0;
   float e[8];
   {
     const f32x4* p = reinterpret_cast<const f32x4*>(partials + o0);
@@ -398,27 +401,28 @@ __global__ __launch_bounds__(256) void prefill_mm_reduce_kernel(const float* __r
   for (int i = 0; i < 8; ++i) {
     o[i] = round_through<OT>(e[i] * kHadScale * f16_to_f32(svh[c0 + i]));
     if (bias) o[i] = round_through<OT>(o[i] + load_as_f32<OT>(bias, c0 + i));
-    store_from_f32<OT>(y, o0 + i, o[i]);
+    store_from_f32<OT>(y, oy + i, o[i]);
   }
 }
 
 template <int OT, int TI>
 static void launch_mm_ti(const MmPlan& p, const uint16_t* xh, const uint16_t* wt, int rows, int k, int n,
-                         const uint16_t* svh, const void* bias, void* y, float* partials, hipStream_t st) {
+                         const uint16_t* svh, const void* bias, void* y, int ldy, float* partials, hipStream_t st) {
   prefill_mm_kernel<OT, TI><<<dim3(p.tiles_m * p.tiles_n, p.splits), kMmThreads, 0, st>>>(
-      xh, wt, rows, k, n, svh, bias, y, p.tiles_m, p.tiles_n, p.splits > 1 ? partials : nullptr, p.steps_per_split);
+      xh, wt, rows, k, n, svh, bias, y, ldy, p.tiles_m, p.tiles_n, p.splits > 1 ? partials : nullptr,
+      p.steps_per_split);
 }
 
 template <int OT>
 static void launch_mm(const MmPlan& p, const uint16_t* xh, const uint16_t* wt, int rows, int k, int n,
-                      const uint16_t* svh, const void* bias, void* y, float* partials, hipStream_t st) {
-  if (p.ti == 4) launch_mm_ti<OT, 4>(p, xh, wt, rows, k, n, svh, bias, y, partials, st);
-  else if (p.ti == 3) launch_mm_ti<OT, 3>(p, xh, wt, rows, k, n, svh, bias, y, partials, st);
-  else launch_mm_ti<OT, 2>(p, xh, wt, rows, k, n, svh, bias, y, partials, st);
+                      const uint16_t* svh, const void* bias, void* y, int ldy, float* partials, hipStream_t st) {
+  if (p.ti == 4) launch_mm_ti<OT, 4>(p, xh, wt, rows, k, n, svh, bias, y, ldy, partials, st);
+  else if (p.ti == 3) launch_mm_ti<OT, 3>(p, xh, wt, rows, k, n, svh, bias, y, ldy, partials, st);
+  else launch_mm_ti<OT, 2>(p, xh, wt, rows, k, n, svh, bias, y, ldy, partials, st);
   if (p.splits > 1) {
     const int groups = rows * (n / 128);
     prefill_mm_reduce_kernel<OT><<<(groups + 15) / 16, 256, 0, st>>>(partials, p.splits, rows, n, groups, svh, bias,
-                                                                     y);
+                                                                     y, ldy);
   }
 }
 
@@ -433,8 +437,8 @@ extern "C" size_t exl3_prefill_matmul_workspace_bytes(int rows, int k, int n) {
 }
 
 extern "C" int exl3_prefill_matmul(const uint16_t* xh, const uint16_t* w_t, int rows, int k, int n,
-                                   const uint16_t* svh, const void* bias, void* y, int out_dtype, void* workspace,
-                                   size_t workspace_bytes, void* stream) {
+                                   const uint16_t* svh, const void* bias, void* y, int ldy, int out_dtype,
+                                   void* workspace, size_t workspace_bytes, void* stream) {
   EXL3_REQUIRE(xh && w_t && svh && y, EXL3_ERR_ARG, "exl3_prefill_matmul: NULL pointer argument");
   EXL3_REQUIRE(k > 0 && k % kMmBK == 0, EXL3_ERR_ARG, "exl3_prefill_matmul: k must be a positive multiple of 64");
   EXL3_REQUIRE(n > 0 && n % 128 == 0, EXL3_ERR_ARG, "exl3_prefill_matmul: n must be a positive multiple of 128");
@@ -442,6 +446,8 @@ extern "C" int exl3_prefill_matmul(const uint16_t* xh, const uint16_t* w_t, int 
   EXL3_REQUIRE(out_dtype >= 0 && out_dtype <= 2, EXL3_ERR_ARG, "exl3_prefill_matmul: bad out_dtype %d", out_dtype);
   EXL3_REQUIRE(aligned(xh, 16) && aligned(w_t, 16) && aligned(y, 16), EXL3_ERR_ARG,
                "exl3_prefill_matmul: xh, w_t and y must be 16-byte aligned");
+  EXL3_REQUIRE(ldy >= n && ((size_t)ldy * (out_dtype == kF32 ? 4 : 2)) % 16 == 0, EXL3_ERR_ARG,
+               "exl3_prefill_matmul: ldy (%d) must be >= n (%d) and keep each row of y 16-byte aligned", ldy, n);
   // (operands below 2 GiB keep every byte offset in 32 bits)
   EXL3_REQUIRE((uint64_t)rows * (uint64_t)k * 2u < (1ull << 31) && (uint64_t)n * (uint64_t)k * 2u < (1ull << 31),
                EXL3_ERR_ARG, "exl3_prefill_matmul: an operand exceeds 2 GiB");
@@ -454,9 +460,9 @@ extern "C" int exl3_prefill_matmul(const uint16_t* xh, const uint16_t* w_t, int 
                "%zu bytes (exl3_prefill_matmul_workspace_bytes), got %zu", p.splits, need, workspace_bytes);
   hipStream_t st = static_cast<hipStream_t>(stream);
   float* part = static_cast<float*>(workspace);
-  if (out_dtype == kF16) launch_mm<kF16>(p, xh, w_t, rows, k, n, svh, bias, y, part, st);
-  else if (out_dtype == kBF16) launch_mm<kBF16>(p, xh, w_t, rows, k, n, svh, bias, y, part, st);
-  else launch_mm<kF32>(p, xh, w_t, rows, k, n, svh, bias, y, part, st);
+  if (out_dtype == kF16) launch_mm<kF16>(p, xh, w_t, rows, k, n, svh, bias, y, ldy, part, st);
+  else if (out_dtype == kBF16) launch_mm<kBF16>(p, xh, w_t, rows, k, n, svh, bias, y, ldy, part, st);
+  else launch_mm<kF32>(p, xh, w_t, rows, k, n, svh, bias, y, ldy, part, st);
   EXL3_LAUNCH_CHECK("exl3_prefill_matmul");
   return EXL3_OK;
 }

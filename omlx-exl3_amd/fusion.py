@@ -30,8 +30,9 @@ kernels and gives the same bits (the prologues compute what exl3_rmsnorm_rotate,
 exl3_rotate write; the epilogue add rounds as torch's fp16 add). bf16 activations take the separate form.
 Prefill rows, ENABLED = False, and layers of any other shape run the model's own forward.
 
-The final norm before an EXL3 output head: the norm and the head's input rotation in one launch (primed into
-the head), then the head's GEMV.
+The final norm before an EXL3 output head: for fp16 decode rows the head's GEMV launch computes the norm in
+its prologue (its statistics from the last layer's block sums) and writes the norm's output, so the head is one
+launch; in the separate form the norm and the head's input rotation run in one launch, then the head's GEMV.
 
 Every tensor handed to model code holds its values, and served or primed results match only the exact tensor
 state they were made for (EXL3Linear.serve / prime), so model code that reads xn, reshapes it or calls a
@@ -277,11 +278,16 @@ class DecodeStep:
 
 
 class HeadNorm:
-    """The final norm before an EXL3 output head, installed as the norm's forward: for decode rows the norm
-    and the head's input rotation in one launch, primed into the head."""
+    """The final norm before an EXL3 output head, installed as the norm's forward. For fp16 decode rows in the
+    prologue form, the head's GEMV launch computes the norm (its statistics from the last layer's block sums
+    of squares when the norm receives exactly that layer's output) and also writes the norm's output, which
+    is returned; the head is served its result for that tensor. Otherwise (the separate form, bf16) the norm
+    and the head's input rotation run in one launch (norm_rot), primed into the head."""
 
-    def __init__(self, norm: nn.Module, head: EXL3Linear):
-        self.norm, self.head = norm, head
+    def __init__(self, norm: nn.Module, head: EXL3Linear, sums: _StreamSums | None = None, form: str = "prologue"):
+        if form not in ("prologue", "separate"):
+            raise ValueError(f"HeadNorm: unknown form {form!r}")
+        self.norm, self.head, self.sums, self.form = norm, head, sums, form
         self.base = norm.forward
         head._prepare()
 
@@ -289,8 +295,17 @@ class HeadNorm:
         rows = x.numel() // x.shape[-1]
         if not ENABLED or rows > MAX_GEMV_ROWS or x.dtype != self.norm.weight.dtype:
             return self.base(x)
-        xn, xh = norm_rot(x.reshape(rows, x.shape[-1]).contiguous(), self.norm.weight,
-                          _rms_eps(self.norm, x.dtype), self.head.rot_suh)
+        k = x.shape[-1]
+        x2 = x.reshape(rows, k).contiguous()
+        eps = _rms_eps(self.norm, x.dtype)
+        if self.form == "prologue" and x.dtype == torch.float16 and "bias" not in self.head:
+            ss = self.sums.take(x) if self.sums is not None else None
+            xn = torch.empty_like(x2)
+            y = self.head.gemv_rmsnorm(x2, None, self.norm.weight, eps, x.dtype, x_sumsq=ss, xn_out=xn)
+            xn = xn.view(x.shape)
+            self.head.serve(xn, y.reshape(x.shape[:-1] + (self.head.out_features,)))
+            return xn
+        xn, xh = norm_rot(x2, self.norm.weight, eps, self.head.rot_suh)
         xn = xn.view(x.shape)
         self.head.prime(xn, xh)
         return xn
@@ -326,7 +341,7 @@ def fuse_decode(model: nn.Module, form: str = "prologue") -> dict[str, int]:
     pair = _head_pair(model)
     if pair is not None:
         norm, head = pair
-        norm.forward = HeadNorm(norm, head)
+        norm.forward = HeadNorm(norm, head, sums=sums, form=form)
         counts["norm"] += 1
         counts["head"] += 1
     return counts

@@ -2,8 +2,8 @@
 """Host-side wrappers of the HIP kernels, mirroring the reference's kernel API
 (src/omlx/exl3/kernels.py): decode_wt, rot, norm_rot, swiglu_rot, TrellisGemvPlan, MAX_GEMV_ROWS, plus
 prefill_gemm (the replacement of decode_wt + matmul + Hadamard on the prefill path: weights reconstructed
-once and a hand-written MFMA GEMM with the output rotation in its epilogue, or one fused launch for small
-grids) and codebook (the codebook diagnostic).
+in bounded column windows, each multiplied by a hand-written MFMA GEMM with the output rotation in its
+epilogue, or one fused launch) and codebook (the codebook diagnostic).
 
 Tensors are torch tensors on the HIP device; every call is enqueued on torch's current stream and returns
 without synchronising. Argument errors raise before anything is launched (the reference asserts,
@@ -13,7 +13,6 @@ from __future__ import annotations
 
 import ctypes
 import math
-import os
 
 import torch
 
@@ -222,6 +221,11 @@ class TrellisGemvPlan:
             _check_out(out, (self.rows, self.n), self.out_dtype)
         return out
 
+    def _check_y(self, out: torch.Tensor, others: list) -> None:
+        """The output is written while other workgroups still read the inputs: it shares no memory with them."""
+        _require(not any(_overlap(out, t) for t in others) and not _overlap(out, self.svh),
+                 "the GEMV output must not overlap its inputs, residual_out, xn_out or y_sumsq (not in place)")
+
     def __call__(self, xh: torch.Tensor, trellises: list[torch.Tensor], bias: torch.Tensor | None = None,
                  out: torch.Tensor | None = None) -> torch.Tensor:
         """trellises: one per member. Returns (rows, n) in out_dtype."""
@@ -231,6 +235,7 @@ class TrellisGemvPlan:
         if self.mixed:
             return self.fused(PROLOGUE_NONE, xh, trellises, bias=bias, out=out)
         out = self._bind(trellises, bias, out, xh.device)
+        self._check_y(out, [xh, bias, *trellises])
         rc = lib().exl3_gemv_ex(ptr(xh), self._tr_c, self.nsub, self._ns_c, self.k, self.K, self.cb, ptr(self.svh),
                                 ptr(bias), ptr(out), DTYPE_CODE[self.out_dtype], self.rows, self.flags,
                                 ptr(self.workspace), self.workspace.numel(), self.kt_per_split,
@@ -272,6 +277,10 @@ class TrellisGemvPlan:
                      "residual_out / xn_out must not overlap x, residual or weight")
         _require(not _overlap(residual_out, xn_out), "residual_out and xn_out must not overlap")
         out = self._bind(trellises, bias, out, x.device)
+        self._check_y(out, [x, residual, residual_out, xn_out, weight, x_sumsq, suh, y_sumsq, bias, *trellises])
+        _require(y_residual is None or not _overlap(out, y_residual) or
+                 (y_residual.data_ptr() == out.data_ptr() and y_residual.numel() == out.numel()),
+                 "y_residual is either the output itself or disjoint from it")
         if self.mixed:
             rc = lib().exl3_gemv_fused_mk(prologue, ptr(x), ptr(residual), ptr(residual_out), ptr(xn_out),
                                           ptr(weight), float(eps), ptr(x_sumsq), ptr(suh), self._tr_c, self.nsub,
@@ -304,50 +313,13 @@ class TrellisGemvPlan:
         return self.fused(PROLOGUE_ROTATE, x, trellises, suh=suh, **kw)
 
 
-# GEMM solution table of the library-GEMM prefill form: PyTorch TunableOp's CSV, made on MI355X by
-# tune_gemm.py for the 27B projection shapes at 16..4608 rows (the fastest hipBLASLt / rocBLAS solution of each
-# shape, which hipBLASLt's default heuristic does not always pick: 15-18% faster GEMMs at 4608 rows).
-GEMM_TABLE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "tuning", "prefill_gemm_mi355x.csv")
-_gemm_table_state: bool | None = None   # None: not read yet
-
-
-def _gemm_table_loaded() -> bool:
-    global _gemm_table_state
-    if _gemm_table_state is None:
-        ok = False
-        if os.path.exists(GEMM_TABLE):
-            try:
-                ok = bool(torch.cuda.tunable.read_file(GEMM_TABLE))   # False if its version lines do not match
-            except RuntimeError:
-                ok = False
-        _gemm_table_state = ok
-    return _gemm_table_state
-
-
-def library_gemm(a: torch.Tensor, wt: torch.Tensor, tuned: bool = True) -> torch.Tensor:
-    """a (rows, k) @ wt (n, k)^T in fp16 with fp32 accumulation, by the process's BLAS library (torch.matmul).
-    With tuned=True and GEMM_TABLE readable, TunableOp is switched on around this one call with tuning off, so
-    a shape in the table runs its recorded solution and any other shape the library default; the caller's
-    TunableOp settings are restored afterwards (nothing is tuned or written)."""
-    if not (tuned and _gemm_table_loaded()):
-        return torch.matmul(a, wt.t())
-    tun = torch.cuda.tunable
-    was_on, was_tuning = tun.is_enabled(), tun.tuning_is_enabled()
-    tun.tuning_enable(False)
-    tun.enable(True)
-    try:
-        return torch.matmul(a, wt.t())
-    finally:
-        tun.enable(was_on)
-        tun.tuning_enable(was_tuning)
-
-
 def prefill_matmul(xh: torch.Tensor, wt: torch.Tensor, svh: torch.Tensor, bias: torch.Tensor | None,
                    out: torch.Tensor) -> torch.Tensor:
-    """had128(xh @ wt^T) * svh (+ bias) into out (rows, n) by the hand-written MFMA GEMM (exl3_prefill_matmul):
-    xh (rows, k) fp16, wt (n, k) fp16 = W_inner^T as exl3_reconstruct writes it. Shapes whose tiles would leave
-    CUs idle split k over several workgroups; their fp32 workspace is allocated here, from PyTorch's caching
-    allocator, for the call."""
+    """had128(xh @ wt^T) * svh (+ bias) into out by the hand-written MFMA GEMM (exl3_prefill_matmul): xh (rows, k)
+    fp16, wt (n, k) fp16 = W_inner^T (or a column window of it) as exl3_reconstruct writes it, svh / bias the n
+    entries of those columns. out is (rows, n), or a column slice of a wider (rows, N) output (its row stride
+    becomes the GEMM's output stride). Shapes whose tiles would leave CUs idle split k over several workgroups;
+    their fp32 workspace is allocated here, from PyTorch's caching allocator, for the call."""
     k = xh.shape[-1]
     rows = xh.numel() // k
     n = wt.shape[0]
@@ -355,28 +327,68 @@ def prefill_matmul(xh: torch.Tensor, wt: torch.Tensor, svh: torch.Tensor, bias: 
              "prefill_matmul: wt must be contiguous fp16 (n, k)")
     _require(k % 64 == 0, "prefill_matmul: k must be a multiple of 64")
     _require(xh.is_contiguous(), "prefill_matmul: xh must be contiguous")
+    _require(out.is_cuda and out.dim() == 2 and tuple(out.shape) == (rows, n) and out.stride(1) == 1,
+             "prefill_matmul: out must be (rows, n) with unit column stride")
+    ldy = out.stride(0) if rows > 1 else n
     nbytes = lib().exl3_prefill_matmul_workspace_bytes(rows, k, n)
     ws = torch.empty(nbytes, dtype=torch.uint8, device=xh.device) if nbytes else None
-    check(lib().exl3_prefill_matmul(ptr(xh), ptr(wt), rows, k, n, ptr(svh), ptr(bias), ptr(out),
+    check(lib().exl3_prefill_matmul(ptr(xh), ptr(wt), rows, k, n, ptr(svh), ptr(bias), ptr(out), ldy,
                                     DTYPE_CODE[out.dtype], ptr(ws), nbytes, stream_handle(xh.device)),
           "exl3_prefill_matmul")
     return out
 
 
-PREFILL_PATHS = ("auto", "matmul", "fused", "library")
+def prefill_out_rotate(g: torch.Tensor, svh: torch.Tensor, bias: torch.Tensor | None,
+                       out: torch.Tensor) -> torch.Tensor:
+    """The output rotation of a prefill product g = xh @ W_inner (rows, n) fp16 computed by some other GEMM:
+    fp16(H128(g)/sqrt(128) * svh) (+ bias) per 128-column block into out (exl3_prefill_out_rotate; the
+    hadamard_transform(y) * svh of linear.py:105)."""
+    _dev(g, "g")
+    rows, n = g.shape
+    _require(g.dtype == torch.float16, "prefill_out_rotate: g must be fp16")
+    _check_vec(svh, n, torch.float16, "svh")
+    _check_vec(bias, n, out.dtype, "bias")
+    _check_out(out, (rows, n), out.dtype)
+    check(lib().exl3_prefill_out_rotate(ptr(g), rows, n, ptr(svh), ptr(bias), ptr(out), DTYPE_CODE[out.dtype],
+                                        stream_handle(g.device)), "exl3_prefill_out_rotate")
+    return out
+
+
+# Bound of the reconstructed W_inner^T the matmul prefill holds per call: the weights are decoded in column
+# windows of at most this many bytes into one buffer, each window multiplied before the next is decoded (the
+# reference decodes at most 16,384 columns at a time, linear.py:28, 97-105). 256 MiB keeps every 27B decoder
+# projection (at most 178 MB) in one window; the output head (5120 -> 151936, 1.56 GB) takes six.
+PREFILL_CHUNK_BYTES = 256 << 20
+_GEMM_OPERAND_LIMIT = 1 << 31      # exl3_prefill_matmul's operands stay below 2 GiB (32-bit buffer offsets)
+_CHUNK_ALIGN = 256                 # the GEMM's tile width in columns
+
+
+def prefill_chunks(n: int, k: int, chunk_bytes: int = PREFILL_CHUNK_BYTES) -> list[tuple[int, int]]:
+    """Column windows (c0, cn) in which the matmul prefill reconstructs W_inner^T: as few windows as keep each
+    window's fp16 (cn, k) within chunk_bytes (and below the GEMM's 2 GiB operand limit), all of one width
+    rounded up to a multiple of 256 columns except a narrower last one. Pure arithmetic (no device work)."""
+    _require(n > 0 and n % 128 == 0 and k > 0, "prefill_chunks: n a positive multiple of 128, k positive")
+    cap = min(chunk_bytes, _GEMM_OPERAND_LIMIT - 1) // (2 * k) // _CHUNK_ALIGN * _CHUNK_ALIGN
+    _require(cap >= _CHUNK_ALIGN, f"prefill_chunks: {chunk_bytes} bytes hold no {_CHUNK_ALIGN}-column window of k={k}")
+    count = -(-n // cap)
+    width = -(-(-(-n // count)) // _CHUNK_ALIGN) * _CHUNK_ALIGN
+    return [(c0, min(width, n - c0)) for c0 in range(0, n, width)]
+
+
+PREFILL_PATHS = ("auto", "matmul", "fused")
 
 
 def prefill_gemm(xh: torch.Tensor, trellis: torch.Tensor, k: int, n: int, K: int, cb: int, svh: torch.Tensor,
                  bias: torch.Tensor | None = None, out_dtype: torch.dtype = torch.float16,
-                 out: torch.Tensor | None = None, path: str = "auto", tuned_gemm: bool = True) -> torch.Tensor:
+                 out: torch.Tensor | None = None, path: str = "auto",
+                 chunk_bytes: int = PREFILL_CHUNK_BYTES) -> torch.Tensor:
     """had128(xh @ W_inner) * svh (+ bias) for xh (rows, k) fp16 (already rotated) (linear.py:97-105).
-    path "matmul": W_inner^T reconstructed once (exl3_reconstruct, bit-exact fp16), then the hand-written MFMA
-    GEMM with the output rotation in its epilogue (exl3_prefill_matmul, k split over workgroups for few rows);
-    "fused": weights reconstructed in LDS and contracted on MFMA in one launch (exl3_prefill_gemm); "auto":
-    "matmul" (k a multiple of 64, as every EXL3 layer's is), else "fused". "library" is the reference's structure with the process's BLAS
-    library for the GEMM - reconstruct, an fp16 GEMM with fp32 accumulation by hipBLASLt through torch.matmul
-    (with tuned_gemm, the solution GEMM_TABLE records for its shape), then the output rotation
-    (exl3_prefill_out_rotate) - kept as a comparison form, not taken by "auto"."""
+    path "matmul": W_inner^T reconstructed (exl3_reconstruct, bit-exact fp16) one column window at a time
+    (prefill_chunks: at most chunk_bytes of fp16 weights alive, one buffer reused), each window multiplied by the
+    hand-written MFMA GEMM with the output rotation in its epilogue (exl3_prefill_matmul, writing its columns of
+    the output in place; k split over workgroups for few rows); "fused": weights reconstructed in LDS and
+    contracted on MFMA in one launch (exl3_prefill_gemm); "auto": "matmul" (k a multiple of 64, as every EXL3
+    layer's is), else "fused"."""
     _dev(xh, "xh")
     rows = xh.numel() // k
     _require(xh.dtype == torch.float16 and xh.numel() == rows * k, "xh must be fp16 (rows, k)")
@@ -393,16 +405,16 @@ def prefill_gemm(xh: torch.Tensor, trellis: torch.Tensor, k: int, n: int, K: int
         _require(not _overlap(out, xh), "prefill_gemm: out must not overlap xh")
     if path == "auto":
         path = "matmul" if k % 64 == 0 else "fused"
-    if path in ("matmul", "library"):
-        wt = torch.empty((n, k), dtype=torch.float16, device=xh.device)
-        check(lib().exl3_reconstruct(ptr(trellis), k, n, K, cb, 0, n // 16, ptr(wt), stream_handle(xh.device)),
-              "exl3_reconstruct")
-        x2 = xh.reshape(rows, k)
-        if path == "matmul":
-            return prefill_matmul(x2.contiguous(), wt, svh, bias, out)
-        g = library_gemm(x2, wt, tuned=tuned_gemm)
-        check(lib().exl3_prefill_out_rotate(ptr(g), rows, n, ptr(svh), ptr(bias), ptr(out), DTYPE_CODE[out_dtype],
-                                            stream_handle(xh.device)), "exl3_prefill_out_rotate")
+    if path == "matmul":
+        chunks = prefill_chunks(n, k, chunk_bytes)
+        x2 = xh.reshape(rows, k).contiguous()
+        y2 = out.view(rows, n)
+        wt = torch.empty((chunks[0][1], k), dtype=torch.float16, device=xh.device)
+        for c0, cn in chunks:
+            w = wt[:cn]
+            check(lib().exl3_reconstruct(ptr(trellis), k, n, K, cb, c0 // 16, cn // 16, ptr(w),
+                                         stream_handle(xh.device)), "exl3_reconstruct")
+            prefill_matmul(x2, w, svh[c0:c0 + cn], None if bias is None else bias[c0:c0 + cn], y2[:, c0:c0 + cn])
         return out
     check(lib().exl3_prefill_gemm(ptr(xh), ptr(trellis), k, n, K, cb, ptr(svh), ptr(bias), ptr(out),
                                   DTYPE_CODE[out_dtype], rows, stream_handle(xh.device)), "exl3_prefill_gemm")
@@ -440,4 +452,5 @@ def attn_decode_rotate(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, k_cach
 
 
 __all__ = ["MAX_GEMV_ROWS", "GEMV_ROWS_LIMIT", "TrellisGemvPlan", "decode_wt", "rot", "norm_rot", "swiglu_rot",
-           "prefill_gemm", "library_gemm", "GEMM_TABLE", "codebook", "attn_decode_rotate", "Exl3Error"]
+           "prefill_gemm", "prefill_chunks", "prefill_matmul", "prefill_out_rotate", "PREFILL_CHUNK_BYTES", "codebook",
+           "attn_decode_rotate", "Exl3Error"]

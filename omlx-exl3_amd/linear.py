@@ -9,10 +9,10 @@ like any layer. Forward computes  y = had128( had128(x * suh) @ W_inner ) * svh 
       other dtypes take a rotation launch first, and a primed rotated input is used as it is), reduces,
       applies the output rotation, svh and the bias, and writes the caller's dtype (kernels.TrellisGemvPlan)
   more rows (prefill, kernels.prefill_gemm): the input rotation, then the reference's sequence on
-      hand-written kernels: W_inner^T reconstructed once (bit-exact fp16), then an MFMA GEMM whose epilogue
-      applies the output rotation, svh and bias (exl3_prefill_matmul); when that GEMM's grid would not fill
-      the GPU (few rows), one launch that reconstructs trellis tiles in LDS, contracts them on MFMA and
-      applies the output rotation, svh and bias (the fp16 weight matrix is never written to memory)
+      hand-written kernels: W_inner^T reconstructed (bit-exact fp16) in column windows of bounded size, as the
+      reference decodes at most 16,384 columns at a time, each window multiplied by an MFMA GEMM whose
+      epilogue applies the output rotation, svh and bias (exl3_prefill_matmul; k split over workgroups for
+      few rows)
 
 EXL3SiblingGroup runs same-input siblings (q/k/v, gate/up) as one GEMV launch over their own trellis
 buffers when they share K and codebook; each member returns its slice of the output, held until every
@@ -272,9 +272,9 @@ class EXL3Linear(nn.Module):
                                                   y_sumsq=y_sumsq)
 
     def _prefill(self, xh: torch.Tensor, out_dtype: torch.dtype, bias: torch.Tensor | None) -> torch.Tensor:
-        """had128(xh @ W_inner) * svh (+ bias) for many rows (linear.py:97-105): reconstruct + hand-written
-        GEMM with the output rotation in its epilogue, or the fused launch when that GEMM's grid would not
-        fill the GPU (kernels.prefill_gemm, path "auto")."""
+        """had128(xh @ W_inner) * svh (+ bias) for many rows (linear.py:97-105): reconstruction in bounded
+        column windows + the hand-written GEMM with the output rotation in its epilogue (kernels.prefill_gemm,
+        path "auto")."""
         return prefill_gemm(xh, self._tr, self.in_features, self.out_features, self._K, self._cb, self._svh,
                             bias=bias, out_dtype=out_dtype)
 

@@ -11,16 +11,16 @@ device generator; suh = +-1, svh = +-1/sqrt(in_features), so that each projectio
 
 Decode runs with a static KV cache (capacity `max_len`) and a device-side position, so one decode step
 has fixed shapes and can be captured in a HIP graph and replayed. The layers are ordinary pre-norm decoder
-layers (h + attn(norm(h)), then h + mlp(norm(h))), so fusion.fuse_decode binds to them like to any
-Llama-shaped model. With fuse=True and fused_attn=True a decode step is five launches per layer
-(exl3_gemv_fused): the q/k/v GEMV with the RMSNorm and input rotations inside it, decode attention
-(exl3_attn_decode_rotate: rotary embedding, cache append, attention and o_proj's input rotation), the o_proj
-GEMV adding its output to the residual stream and writing the stream's 128-block sums of squares, the
-gate/up GEMV with its RMSNorm inside it (reading those sums), and the down_proj GEMV with the SwiGLU inside it
-and the residual add after it; the output head's GEMV takes the final norm the same way. With fuse=True and
-fused_attn=False the layers run fusion.DecodeStep around attention as torch operations; with fuse=False the
-model's own modules (torch RMSNorm, SiLU and adds, EXL3Linear calls). Prefill attention uses torch
-operations on fp16 tensors.
+layers (h + attn(norm(h)), then h + mlp(norm(h))), and fusion.fuse_decode binds to them as to any
+Llama-shaped model: every decode step runs through fusion.DecodeStep and HeadNorm. With fuse=True and
+fused_attn=True a decode step is five launches per layer (exl3_gemv_fused): the q/k/v GEMV with the RMSNorm
+and input rotations inside it, decode attention (exl3_attn_decode_rotate: rotary embedding, cache append,
+attention and o_proj's input rotation), the o_proj GEMV adding its output to the residual stream and writing
+the stream's 128-block sums of squares, the gate/up GEMV with its RMSNorm inside it (reading those sums), and
+the down_proj GEMV with the SwiGLU inside it and the residual add after it; the output head's GEMV takes the
+final norm the same way. fuse_form="separate" runs DecodeStep's separate-kernel form (the same bits); with
+fused_attn=False attention runs as torch operations; with fuse=False the model's own modules (torch RMSNorm,
+SiLU and adds, EXL3Linear calls). Prefill attention uses torch operations on fp16 tensors.
 """
 from __future__ import annotations
 
@@ -204,7 +204,7 @@ class SyntheticDecoder(nn.Module):
     and returns the logits of the last one (vocab,) in fp32."""
 
     def __init__(self, cfg: DecoderConfig, seed: int = 0, device="cuda", fuse: bool = True, fused_attn: bool = True,
-                 gemv_prologues: bool = True):
+                 fuse_form: str = "prologue"):
         super().__init__()
         self.cfg = cfg
         gen = torch.Generator(device=device)
@@ -225,46 +225,14 @@ class SyntheticDecoder(nn.Module):
         self.register_buffer("rope_sin_half", sin[:, :half].contiguous(), persistent=False)
         self.requires_grad_(False)
         self.groups = group_siblings(self)
-        self.fused = fuse_decode(self) if fuse else {}
-        self.gemv_prologues = gemv_prologues     # decode: norms and SwiGLU inside the GEMV launches
+        # decode steps through fusion.DecodeStep / HeadNorm, the path any Llama-shaped model gets from
+        # fuse_decode: form "prologue" puts the norms, SwiGLU and residual adds inside the GEMV launches
+        self.fused = fuse_decode(self, form=fuse_form) if fuse else {}
         for layer in self.model.layers:
             layer.self_attn.fused_attn = fused_attn
 
-    def _decode_fused(self, ids: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
-        """One decode step (T = 1) with the norms and the SwiGLU inside the GEMV launches; the same values,
-        bit for bit, as the layer-by-layer path."""
-        # the residual stream h: each layer's o_proj and down_proj GEMVs add their output to it in their
-        # epilogue and write its 128-block sums of squares, which the next norm (inside the next GEMV) reads
-        h = self.model.embed_tokens(ids)                                           # (1, hidden)
-        dt = h.dtype
-        ss = None                                                                  # block sums of squares of h
-        n_blk = self.cfg.hidden // 128
-        for layer in self.model.layers:
-            attn, mlp = layer.self_attn, layer.mlp
-            ln1, ln2 = layer.input_layernorm, layer.post_attention_layernorm
-            qkv = attn.q_proj._group.gemv_rmsnorm(h, None, ln1.weight, ln1.eps, dt, x_sumsq=ss)
-            q, k, v = torch.split(qkv, attn.q_proj._group.ns, dim=-1)
-            xh, _ = attn_decode_rotate(q.reshape(-1), k.reshape(-1), v.reshape(-1), attn.k_cache, attn.v_cache, pos,
-                                       self.rope_cos_half, self.rope_sin_half, attn.o_proj.rot_suh.reshape(-1))
-            ss = torch.empty((1, n_blk), dtype=torch.float64, device=h.device)
-            h = attn.o_proj.gemv_rotated(xh, dt, attn.o_proj._bias_for(dt), y_residual=h, y_sumsq=ss)
-            gu = mlp.gate_proj._group.gemv_rmsnorm(h, None, ln2.weight, ln2.eps, torch.float16, x_sumsq=ss)
-            ss = torch.empty((1, n_blk), dtype=torch.float64, device=h.device)
-            h = mlp.down_proj.gemv_swiglu(gu, dt, y_residual=h, y_sumsq=ss)
-        norm = self.model.norm
-        return self.lm_head.gemv_rmsnorm(h, None, norm.weight, norm.eps, dt, x_sumsq=ss).float().reshape(-1)
-
-    def _fused_decode_ok(self, T: int) -> bool:
-        if T != 1 or not self.fused or not self.gemv_prologues or self.model.embed_tokens.weight.dtype != torch.float16:
-            return False
-        layer = self.model.layers[0]
-        return (layer.self_attn.fused_attn and layer.self_attn.q_proj._group is not None
-                and layer.mlp.gate_proj._group is not None and "bias" not in self.lm_head)
-
     @torch.no_grad()
     def forward(self, ids: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
-        if self._fused_decode_ok(ids.shape[0]):
-            return self._decode_fused(ids, pos)
         h = self.model.embed_tokens(ids)                                           # (T, hidden)
         for layer in self.model.layers:
             h = layer(h, pos, self.rope_cos, self.rope_sin, self.rope_cos_half, self.rope_sin_half)

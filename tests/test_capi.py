@@ -58,8 +58,10 @@ def test_argument_errors(capi):
     # gemv: members, n % 128, rows, flags, workspace
     trs = (ctypes.c_void_p * 3)(0x1000, 0x1000, 0x1000)
     ns = (ctypes.c_int * 3)(128, 128, 128)
-    args = dict(xh=p, tr=trs, nm=1, ns=ns, k=1024, K=6, cb=0, svh=p, bias=None, y=p, ot=0, rows=1, flags=0,
-                ws=None, wsb=0, st=None)
+    # (disjoint device addresses: the output may not overlap an input)
+    xh_p, svh_p, y_p = (ctypes.c_void_p(0x100000 * i) for i in (1, 2, 3))
+    args = dict(xh=xh_p, tr=trs, nm=1, ns=ns, k=1024, K=6, cb=0, svh=svh_p, bias=None, y=y_p, ot=0, rows=1,
+                flags=0, ws=None, wsb=0, st=None)
 
     def gemv(**kw):
         a = dict(args, **kw)
@@ -82,15 +84,22 @@ def test_argument_errors(capi):
     ns_gu = (ctypes.c_int * 3)(17408, 17408, 0)
     assert lib.exl3_gemv_noalloc(p, trs, 2, ns_gu, 5120, 6, 0, p, None, p, 0, 16, 0, None) == -2
     assert "scratch" in _err(capi)
+    # the 27B output head (5120 -> 151936, 7 splits): its partials fit the fixed scratch at 1 row only
+    ns_head = (ctypes.c_int * 3)(151936, 0, 0)
+    assert lib.exl3_gemv_noalloc(xh_p, trs, 1, ns_head, 5120, 6, 0, svh_p, None, y_p, 0, 2, 0, None) == -2
+    assert "scratch" in _err(capi)
+    assert lib.exl3_gemv_noalloc(xh_p, trs, 1, ns_head, 5120, 6, 0, svh_p, None, y_p, 0, 1, 0, None) != -2
     # rotations
     assert lib.exl3_rotate(p, 0, p, 1, 1, 100, p, None) == -1 and "128" in _err(capi)
     assert lib.exl3_rotate(p, 5, p, 1, 1, 128, p, None) == -1
     assert lib.exl3_rmsnorm_rotate(p, None, None, p, 2, 1e-6, p, 1, 1, 128, p, p, None) == -1
     assert lib.exl3_swiglu_rotate(p, p, 1, 100, p, None) == -1
     assert lib.exl3_prefill_gemm(p, p, 64, 100, 6, 0, p, None, p, 0, 4, None) == -1
-    # hand-written prefill GEMM: k % 64, n % 128, rows, NULL, alignment, out dtype, 2 GiB operands, workspace
-    def mm(xh, wt, rows, k, n, svh, bias, y, ot, ws=None, wsb=0):
-        return lib.exl3_prefill_matmul(xh, wt, rows, k, n, svh, bias, y, ot, ws, wsb, None)
+    # hand-written prefill GEMM: k % 64, n % 128, rows, NULL, alignment, out dtype, output row stride, 2 GiB
+    # operands, workspace
+    def mm(xh, wt, rows, k, n, svh, bias, y, ot, ws=None, wsb=0, ldy=None):
+        return lib.exl3_prefill_matmul(xh, wt, rows, k, n, svh, bias, y, n if ldy is None else ldy, ot, ws, wsb,
+                                       None)
 
     assert mm(p, p, 4, 96, 128, p, None, p, 0) == -1 and "multiple of 64" in _err(capi)
     assert mm(p, p, 4, 64, 100, p, None, p, 0) == -1 and "multiple of 128" in _err(capi)
@@ -98,6 +107,9 @@ def test_argument_errors(capi):
     assert mm(None, p, 4, 64, 128, p, None, p, 0) == -1 and "NULL" in _err(capi)
     assert mm(ctypes.c_void_p(0x1008), p, 4, 64, 128, p, None, p, 0) == -1 and "aligned" in _err(capi)
     assert mm(p, p, 4, 64, 128, p, None, p, 3) == -1 and "out_dtype" in _err(capi)
+    assert mm(p, p, 4, 64, 256, p, None, p, 0, ldy=128) == -1 and "ldy" in _err(capi)   # rows overlap
+    assert mm(p, p, 4, 64, 128, p, None, p, 0, ldy=132) == -1 and "ldy" in _err(capi)   # 264-byte rows
+    assert mm(p, p, 4, 64, 128, p, None, p, 2, ldy=130) == -1 and "ldy" in _err(capi)   # fp32: 520-byte rows
     assert mm(p, p, 1 << 20, 1024, 128, p, None, p, 0) == -1 and "2 GiB" in _err(capi)
     assert mm(p, p, 1 << 23, 64, 1 << 23, p, None, p, 0) == -1 and "tiles" in _err(capi)   # 2^31 tiles
     # few rows: k is split over workgroups, which needs the workspace the query reports
@@ -145,6 +157,41 @@ def test_overlapping_outputs_are_rejected(capi):
     assert fused(2, x, None, None, xn, None, None) == -1 and "xn_out" in _err(capi)
     assert fused(3, x, None, None, None, w, None) == -1 and "ROTATE" in _err(capi)
     assert fused(4, x, None, None, None, None, None) == -1 and "prologue" in _err(capi)
+
+
+def test_gemv_output_overlapping_an_input_is_rejected(capi):
+    """y is written by each block's last workgroup while other workgroups still read the inputs, so the GEMV
+    entry points refuse a y that shares memory with xh / x, residual, w, suh, svh, bias, a trellis, the norm
+    outputs or y_sumsq (host-side check, before any launch); y_residual may be y itself but not a shifted view."""
+    lib = capi.lib()
+    base = 0x1000000
+    xh, svh, y, x, w, suh, res, ss = (ctypes.c_void_p(base + i * 0x100000) for i in range(8))
+    trs = (ctypes.c_void_p * 3)(base + 0x800000, base + 0x800000, base + 0x800000)
+    ns = (ctypes.c_int * 3)(256, 0, 0)
+    k, rows = 1024, 2
+
+    def gemv(xh_=xh, y_=y, svh_=svh, bias=None, tr=trs):
+        return lib.exl3_gemv(xh_, tr, 1, ns, k, 6, 0, svh_, bias, y_, 0, rows, 0, None, 0, None)
+
+    assert gemv() == -2                                                   # disjoint: on to the workspace check
+    assert gemv(y_=xh) == -1 and "overlap" in _err(capi)                  # in place
+    assert gemv(y_=ctypes.c_void_p(base + 0x100)) == -1                   # y inside xh
+    assert gemv(y_=ctypes.c_void_p(base + 0x100000 - 0x200)) == -1        # y runs into svh
+    assert gemv(bias=ctypes.c_void_p(base + 0x200200)) == -1              # bias inside y (rows x 256 fp16)
+    assert gemv(y_=ctypes.c_void_p(base + 0x800400)) == -1                # y inside the trellis
+
+    def fused(pro, xx, y_, yres=None, yss=None, resid=None):
+        return lib.exl3_gemv_fused(pro, xx, resid, None, None, w if pro == 1 else None, 1e-6, None, suh, trs, 1,
+                                   ns, k, 6, 0, svh, None, y_, 0, rows, 0, yres, yss, None, 0, None)
+
+    assert fused(1, x, y) == -2
+    assert fused(1, x, x) == -1 and "overlap" in _err(capi)               # RMSNORM in place
+    assert fused(1, x, w) == -1                                           # y on the norm weight
+    assert fused(1, x, y, resid=y) == -1                                  # y on the residual
+    assert fused(3, x, suh) == -1                                         # y on the signs
+    assert fused(1, x, y, yres=y) == -2                                   # the residual add in place: allowed
+    assert fused(1, x, y, yres=ctypes.c_void_p(base + 0x200000 + 0x80)) == -1 and "y_residual" in _err(capi)
+    assert fused(1, x, y, yss=ctypes.c_void_p(base + 0x200000 + 0x40)) == -1   # sums of squares inside y
 
 
 def test_gemv_fused_mk_argument_errors(capi):

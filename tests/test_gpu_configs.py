@@ -1,12 +1,12 @@
 """GPU parity at the benchmark's full sizes for the two largest configurations:
 
   config 4  prefill contraction, M = 4608 rows through gate/up (5120 -> 17408) and down (17408 -> 5120) at K = 6,
-            both prefill forms (the library form with its GEMM solution table, as the benchmark times it, and
+            both prefill forms (reconstruction + the hand-written MFMA GEMM, as the benchmark times it, and
             the fused reconstruct-in-LDS kernel), against had128(xh @ W_inner) * svh in fp32 with W_inner from
             decode_wt (bit-exact, oracle-pinned), bar max-abs-rel 2e-3 (the GEMV/GEMM bar);
   config 5  the 64-layer synthetic 27B-shape decoder: graph replay equals eager decoding bit for bit, the
-            five-launch decode step equals the layer-by-layer step (fusion.DecodeStep around the same
-            attention kernel) bit for bit, and prompt prefill (512 tokens) and the first decode steps agree
+            five-launch decode step (fuse_decode's DecodeStep, prologue form) equals DecodeStep's
+            separate-kernel form around the same attention kernel bit for bit, and prompt prefill (512 tokens) and the first decode steps agree
             with an fp32 formulation of the same model, built layer by layer from decode_wt weights (one
             projection reconstructed at a time), within 2% of the logit range."""
 import math
@@ -34,7 +34,7 @@ def _had128_t(v):
 
 # ------------------------------------------------------------------------------------------ config 4
 @pytest.mark.parametrize("shape", ["gate_up", "down"])
-@pytest.mark.parametrize("path", ["matmul", "library", "fused"])
+@pytest.mark.parametrize("path", ["matmul", "fused"])
 def test_config4_prefill_4608_rows(pk, shape, path):
     k, n = (5120, 17408) if shape == "gate_up" else (17408, 5120)
     K, rows = 6, 4608
@@ -49,7 +49,7 @@ def test_config4_prefill_4608_rows(pk, shape, path):
     del W
     err = ((y - ref).abs().max() / ref.abs().max()).item()
     assert err < 2e-3, err
-    if path in ("library", "matmul"):   # deterministic, and fp16 output within the bar of the fp32 output
+    if path == "matmul":   # deterministic, and fp16 output within the bar of the fp32 output
         y16 = pk.kernels.prefill_gemm(xh, tr, k, n, K, 0, svh, out_dtype=torch.float16, path=path)
         assert ((y16.float() - ref).abs().max() / ref.abs().max()).item() < 2e-3
         assert torch.equal(pk.kernels.prefill_gemm(xh, tr, k, n, K, 0, svh, out_dtype=torch.float32, path=path), y)
@@ -101,9 +101,9 @@ def test_config5_graph_replay_equals_eager_and_prologues_equal_layer_by_layer(pk
         greedy_step(model, tok, pos)
         eager.append(model.last_logits.clone())
         toks.append(tok.clone())
-    # the layer-by-layer form: DecodeStep around the same attention kernel
+    # DecodeStep's separate-kernel form around the same attention kernel
     _restore(model, snap)
-    model.gemv_prologues = False
+    pk.fusion.fuse_decode(model, form="separate")
     try:
         tok, pos = first.clone(), torch.tensor([PROMPT], device="cuda")
         for i in range(4):
@@ -111,7 +111,7 @@ def test_config5_graph_replay_equals_eager_and_prologues_equal_layer_by_layer(pk
             assert torch.equal(model.last_logits, eager[i]), i
             assert torch.equal(tok, toks[i]), i
     finally:
-        model.gemv_prologues = True
+        pk.fusion.fuse_decode(model)
     # one captured graph replayed
     _restore(model, snap)
     tok, pos = first.clone(), torch.tensor([PROMPT], device="cuda")

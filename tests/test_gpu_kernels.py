@@ -333,7 +333,7 @@ def test_gemv_bias_and_split_override(pk):
 
 
 # ------------------------------------------------------------------------------------------ prefill
-@pytest.mark.parametrize("path", ["matmul", "fused", "library"])
+@pytest.mark.parametrize("path", ["matmul", "fused"])
 @pytest.mark.parametrize("K,cb", [(6, 0), (4, 1), (3, 2), (8, 0)])
 def test_prefill_vs_oracle(pk, K, cb, path):
     k, n, rows = 512, 384, 200
@@ -347,8 +347,7 @@ def test_prefill_vs_oracle(pk, K, cb, path):
         assert O.max_abs_rel(y.float().cpu().numpy(), ref) < bar, (dt,)
 
 
-@pytest.mark.parametrize("path,rows", [("fused", 512), ("library", 512), ("library", 1100), ("matmul", 512),
-                                       ("matmul", 1100)])
+@pytest.mark.parametrize("path,rows", [("fused", 512), ("matmul", 512), ("matmul", 1100)])
 def test_prefill_27b_shape_vs_reconstruct(pk, path, rows):
     k, n, K = 5120, 17408, 6
     g = torch.Generator(device="cuda").manual_seed(3)
@@ -362,47 +361,79 @@ def test_prefill_27b_shape_vs_reconstruct(pk, path, rows):
 
 
 @pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16, torch.float32])
-def test_prefill_library_path_matches_fused_with_bias(pk, dt):
-    """The three prefill forms with a bias and every output dtype, ragged row count (not a multiple of the
-    GEMM or rotation tiles): within the GEMM bar of each other; the library and matmul forms are
-    deterministic."""
+def test_prefill_forms_match_with_bias(pk, dt):
+    """The two prefill forms with a bias and every output dtype, ragged row count (not a multiple of the
+    GEMM or rotation tiles): within the GEMM bar of each other; both are deterministic."""
     k, n, K, rows = 1024, 640, 5, 777
     rng = np.random.default_rng(21)
     tr = dev(O.random_trellis(k, n, K, 31))
     svh = dev((rng.standard_normal(n) * 0.02).astype(np.float16))
     bias = dev(rng.standard_normal(n).astype(np.float32)).to(dt)
     xh = dev(rng.standard_normal((rows, k)).astype(np.float16))
-    paths = ("fused", "library", "matmul")
+    paths = ("fused", "matmul")
     ys = [pk.kernels.prefill_gemm(xh, tr, k, n, K, 1, svh, bias=bias, out_dtype=dt, path=p) for p in paths]
     bar = 1e-2 if dt == torch.bfloat16 else 2e-3
-    for y in ys[1:]:
-        assert O.max_abs_rel(y.float().cpu().numpy(), ys[0].float().cpu().numpy()) < bar
-    for i in (1, 2):
+    assert O.max_abs_rel(ys[1].float().cpu().numpy(), ys[0].float().cpu().numpy()) < bar
+    for i in (0, 1):
         again = pk.kernels.prefill_gemm(xh, tr, k, n, K, 1, svh, bias=bias, out_dtype=dt, path=paths[i])
         assert torch.equal(again, ys[i]), paths[i]
 
 
-def test_prefill_tuned_gemm_matches_default_and_restores_tunableop(pk):
-    """The library form with the GEMM solution table (a 27B down_proj shape the table lists at 512 rows) against
-    the library default: within the GEMM bar of each other and of the oracle-built product; TunableOp's
-    switches are back to the caller's values afterwards."""
+@pytest.mark.parametrize("dt", [torch.float16, torch.float32])
+def test_prefill_column_windows_equal_one_window(pk, dt):
+    """The matmul prefill with its weights reconstructed in several column windows (a small window bound: four
+    windows of 512 columns and a narrower last one, each GEMM writing its slice of the output in place, with a
+    bias) gives the bits of the same call in one window, and matches the oracle."""
+    k, n, K, rows = 1024, 2176, 6, 640
+    chunks = pk.kernels.prefill_chunks(n, k, chunk_bytes=512 * k * 2)
+    assert len(chunks) == 5 and chunks[0] == (0, 512) and chunks[-1] == (2048, 128)
+    rng = np.random.default_rng(5)
+    tr_np = O.random_trellis(k, n, K, 17)
+    tr = dev(tr_np)
+    svh_np = (rng.standard_normal(n) * 0.02).astype(np.float16)
+    svh = dev(svh_np)
+    bias = dev(rng.standard_normal(n).astype(np.float32)).to(dt)
+    xh_np = rng.standard_normal((rows, k)).astype(np.float16)
+    xh = dev(xh_np)
+    one = pk.kernels.prefill_gemm(xh, tr, k, n, K, 0, svh, bias=bias, out_dtype=dt, path="matmul")
+    many = pk.kernels.prefill_gemm(xh, tr, k, n, K, 0, svh, bias=bias, out_dtype=dt, path="matmul",
+                                   chunk_bytes=512 * k * 2)
+    assert torch.equal(one, many)
+    ref = O.gemv_ref(xh_np, O.reconstruct_inner(tr_np, k, n, K, 0), svh_np)
+    got = many.float().cpu().numpy() - bias.float().cpu().numpy()
+    bar = 2e-3 if dt == torch.float32 else 4e-3   # fp16 output: the bias add rounds once more
+    assert O.max_abs_rel(got, ref) < bar
+
+
+def test_prefill_output_head_in_bounded_windows(pk):
+    """The 27B output head, 5120 -> 151936 at K = 6 (1.56 GB of fp16 W_inner^T, which the GEMM would refuse past
+    2 GiB for a larger head if it were built whole) at 64 rows: reconstructed in six column windows of at most
+    PREFILL_CHUNK_BYTES, each multiplied into its slice of the output; against the fp32 product of decode_wt's
+    weights, window by window (each boundary at 25344 j is crossed), bar 2e-3. The call's transient device
+    memory is bounded by one window plus a small GEMM workspace."""
+    k, n, K, rows = 5120, 151936, 6, 64
     F = pk.kernels
-    tun = torch.cuda.tunable
-    before = (tun.is_enabled(), tun.tuning_is_enabled())
-    k, n, K, rows = 17408, 5120, 6, 512
-    g = torch.Generator(device="cuda").manual_seed(22)
+    chunks = F.prefill_chunks(n, k)
+    assert len(chunks) == 6 and all(cn * k * 2 <= F.PREFILL_CHUNK_BYTES for _, cn in chunks)
+    print(f"output head prefill {k}->{n} rows {rows}: windows {chunks}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(151)
     tr = torch.randint(-32768, 32768, (k // 16, n // 16, 16 * K), dtype=torch.int16, device="cuda", generator=g)
     svh = (torch.randn(n, device="cuda", generator=g) * 0.01).half()
     xh = torch.randn((rows, k), device="cuda", generator=g).half()
-    y_def = F.prefill_gemm(xh, tr, k, n, K, 0, svh, out_dtype=torch.float32, path="library", tuned_gemm=False)
-    y_tab = F.prefill_gemm(xh, tr, k, n, K, 0, svh, out_dtype=torch.float32, path="library", tuned_gemm=True)
-    assert (tun.is_enabled(), tun.tuning_is_enabled()) == before
-    assert ((y_tab - y_def).abs().max() / y_def.abs().max()).item() < 2e-3
-    W = F.decode_wt(tr, k, n, K, 0).float()
-    ref = _had128_t(xh.float() @ W.T) * svh.float()
-    assert ((y_tab - ref).abs().max() / ref.abs().max()).item() < 2e-3
-    if not F._gemm_table_loaded():
-        pytest.skip("GEMM solution table not accepted by this PyTorch / ROCm build (its version lines differ)")
+    out = torch.empty((rows, n), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats()
+    base = torch.cuda.memory_allocated()
+    F.prefill_gemm(xh, tr, k, n, K, 0, svh, out_dtype=torch.float32, out=out)
+    torch.cuda.synchronize()
+    transient = torch.cuda.max_memory_allocated() - base
+    assert transient <= chunks[0][1] * k * 2 + (64 << 20), transient
+    for c0, cn in chunks:
+        W = F.decode_wt(tr, k, n, K, 0, nt0=c0 // 16, ntc=cn // 16).float()
+        ref = _had128_t(xh.float() @ W.T) * svh[c0:c0 + cn].float()
+        del W
+        err = ((out[:, c0:c0 + cn] - ref).abs().max() / ref.abs().max()).item()
+        assert err < 2e-3, (c0, err)
 
 
 @pytest.mark.parametrize("rows,n,k,ti", [(4500, 17408, 128, 4), (4608, 17536, 64, 4), (4500, 5120, 256, 3),
@@ -609,7 +640,7 @@ def test_gemv_small_and_ragged_k(pk, k, ns, K):
         assert O.max_abs_rel(y.cpu().numpy(), ref) < 2e-3, (k, ns, K, rows)
 
 
-@pytest.mark.parametrize("rows,path", [(9, "fused"), (9, "library"), (9, "auto"), (63, "fused"), (64, "auto"),
+@pytest.mark.parametrize("rows,path", [(9, "fused"), (9, "auto"), (63, "fused"), (64, "auto"),
                                        (1, "matmul"), (9, "matmul"), (63, "matmul"), (129, "matmul")])
 def test_prefill_row_count_edges(pk, rows, path):
     """The smallest prefill row count through both forms and the default, and a few more row counts,

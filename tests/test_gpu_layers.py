@@ -128,7 +128,7 @@ def test_synthetic_decode_forms_and_their_launches(pk):
     toks = [torch.tensor([7], device="cuda") for _ in range(3)]
     poss = [torch.tensor([12], device="cuda") for _ in range(3)]
     want = {0: {"exl3_gemv_fused": 4 * L + 1, "exl3_attn_decode_rotate": L},
-            1: {"exl3_gemv_fused": 4 * L, "exl3_rmsnorm_rotate": 1, "exl3_gemv_ex": 1},
+            1: {"exl3_gemv_fused": 4 * L + 1},
             2: {"exl3_gemv_fused": 4 * L + 1}}
     for _ in range(4):
         outs = []

@@ -95,15 +95,16 @@ MIXED_K = {"q_proj": 6, "k_proj": 3, "v_proj": 8, "o_proj": 4, "gate_proj": 5, "
 
 @pytest.mark.parametrize("kmap", [None, MIXED_K], ids=["K6", "mixedK"])
 def test_decoder_gemv_prologues_match_layer_by_layer(pk, kmap):
-    """The five-launch decode step (norms, SwiGLU and residual adds inside the GEMV launches) equals the
-    layer-by-layer step bit for bit, also with every projection at its own bitrate (q/k/v and gate/up then
-    run as mixed-width launches)."""
+    """The five-launch decode step (fuse_decode's DecodeStep and HeadNorm in the prologue form: norms, SwiGLU
+    and residual adds inside the GEMV launches) equals their separate-kernel form (norm_rot, swiglu_rot,
+    torch adds around the GEMVs) bit for bit, also with every projection at its own bitrate (q/k/v and gate/up
+    then run as mixed-width launches)."""
     from omlx_exl3_amd.synthetic import DecoderConfig, SyntheticDecoder, greedy_step
 
     cfg = DecoderConfig(n_layers=3, hidden=512, intermediate=1024, n_heads=4, n_kv_heads=2, head_dim=128,
                         vocab=2048, max_len=64, K_by_proj=kmap)
     deep = SyntheticDecoder(cfg, seed=8, device="cuda")
-    layered = SyntheticDecoder(cfg, seed=8, device="cuda", gemv_prologues=False)
+    layered = SyntheticDecoder(cfg, seed=8, device="cuda", fuse_form="separate")
     if kmap:
         att = deep.model.layers[0].self_attn
         assert att.q_proj._group is not None and att.q_proj._group.Ks == [6, 3, 8]

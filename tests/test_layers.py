@@ -309,26 +309,33 @@ def test_synthetic_decoder_structure():
     assert synthetic.greedy_step.argmax(v).item() == 300
 
 
-def test_prefill_gemm_table_is_well_formed():
-    """The library prefill form's GEMM solution table (TunableOp CSV): version lines for this PyTorch build and
-    gfx950, and one entry per 27B projection shape at the row counts the benchmarks use (512, 4608), each
-    naming a hipBLASLt / rocBLAS solution or the library default. The GEMM is torch.matmul(x, wt.t()) with x
-    (rows, k) and wt (n, k), which PyTorch runs as the column-major "TN" product of M = n, N = rows, K = k."""
+def test_prefill_column_windows():
+    """The matmul prefill's column windows (prefill_chunks, no device work): each window's fp16 W_inner^T within
+    the byte bound and below the GEMM's 2 GiB operand limit, windows of one width (a multiple of the 256-column
+    GEMM tile) covering [0, n) in order, the last one narrower. Every 27B decoder projection fits in one window;
+    the output head and shapes whose whole W^T exceeds 2 GiB are split."""
     from omlx_exl3_amd import kernels
-    lines = [ln.strip().split(",") for ln in open(kernels.GEMM_TABLE) if ln.strip()]
-    val = {f[1]: f[2] for f in lines if f[0] == "Validator"}
-    assert val["PT_VERSION"] == torch.__version__.split("+")[0]
-    assert val["GCN_ARCH_NAME"].startswith("gfx950")
-    assert "HIPBLASLT_VERSION" in val and "ROCBLAS_VERSION" in val
-    entries = {f[1]: f[2] for f in lines if f[0] == "GemmTunableOp_Half_TN"}
-    assert len(entries) + len(val) == len(lines)
-    for rows in (512, 4608):
-        for k, n in [(5120, 6144), (5120, 1024), (6144, 5120), (5120, 17408), (17408, 5120)]:
-            sol = entries[f"tn_{n}_{rows}_{k}_ld_{k}_{k}_{n}"]
-            assert sol == "Default" or sol.split("_")[:2] in (["Gemm", "Hipblaslt"], ["Gemm", "Rocblas"])
+    cases = [(6144 + 2048, 5120), (5120, 6144), (34816, 5120), (5120, 17408), (151936, 5120), (152064, 8192),
+             (262144, 17408), (128, 64), (384, 1024)]
+    for n, k in cases:
+        ch = kernels.prefill_chunks(n, k)
+        assert ch[0][0] == 0 and sum(cn for _, cn in ch) == n
+        assert all(a + an == b for (a, an), (b, _) in zip(ch, ch[1:]))
+        assert all(cn * k * 2 <= kernels.PREFILL_CHUNK_BYTES and cn * k * 2 < 2 ** 31 for _, cn in ch)
+        assert all(cn == ch[0][1] and cn % 256 == 0 for _, cn in ch[:-1]) and 0 < ch[-1][1] <= ch[0][1]
+        assert all(cn % 128 == 0 for _, cn in ch)
+        if n * k * 2 <= kernels.PREFILL_CHUNK_BYTES:
+            assert ch == [(0, n)]
+    assert kernels.prefill_chunks(151936, 5120) == [(25344 * j, 25344) for j in range(5)] + [(126720, 25216)]
+    # an 8192 -> 152064 head is 2.49 GB of fp16 weights: never built whole
+    big = kernels.prefill_chunks(152064, 8192)
+    assert len(big) > 1 and max(cn for _, cn in big) * 8192 * 2 < 2 ** 31
+    # a smaller bound gives more windows; a bound below one tile is refused
+    assert len(kernels.prefill_chunks(2176, 1024, chunk_bytes=512 * 1024 * 2)) == 5
+    with pytest.raises(ValueError):
+        kernels.prefill_chunks(2176, 1024, chunk_bytes=1000)
 
 
-# ------------------------------------------------------------------------------------------ slots, row-exactness
 def test_slot_matches_only_the_same_tensor_state():
     x = torch.randn(2, 256, dtype=torch.float16)
     slot = linear._Slot()

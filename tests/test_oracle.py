@@ -229,6 +229,30 @@ def test_rmsnorm_rotate_vs_textbook(bf16, residual):
     assert _rel(xh, ref) < 1e-3
 
 
+@pytest.mark.parametrize("bf16", [False, True])
+def test_rmsnorm_rounding_known_answer(bf16):
+    """MLX's rms_norm rounding, xn = T(w * T(h * inv)) (reference kernels.py:422), on a case worked out by hand,
+    where rounding h * inv before the weight multiply and rounding only once, T(w * h * inv), give different
+    bits. Row h = [1, 3 x 127] (KD = 128), eps = 1/16: sum h^2 / KD = 1144 / 128 = 8.9375 exactly, + eps = 9,
+    so inv = 1/sqrt(9) = fp32(1/3) = 0x3EAAAAAB = 0.3333333432674408; w = 1.25 everywhere.
+      fp16, element 0: h * inv = 0.33333334 -> T = 0x3555 = 0.333251953125; w * that = 0.41656494140625 (exact
+        in fp32) = 1706.25 steps of 2^-12 -> 0x36AA = 0.41650390625. Rounded once: 1.25 * 0.33333334 =
+        0.41666668 = 1706.67 steps -> 0x36AB.
+      bf16, element 0: T(0.33333334) = 0x3EAB = 0.333984375; * 1.25 = 0.41748046875 = 213.75 steps of 2^-9 ->
+        0x3ED6 = 0.41796875. Rounded once: 0.41666668 = 213.33 steps -> 0x3ED5.
+      elements 1..127: 3 * inv = 1 + 2^-25 -> fp32 1.0 -> T = 1.0, * 1.25 = 1.25 (fp16 0x3D00, bf16 0x3FA0)
+        under either recipe.
+    An eps added in the wrong place (to the sum, or after the square root) moves inv off 1/3 and every element
+    off these values."""
+    x = np.array([[1.0] + [3.0] * 127], dtype=np.float32)
+    w = np.full(128, 1.25, dtype=np.float32)
+    conv = (lambda a: O.f32_to_bf16_bits(a)) if bf16 else (lambda a: a.astype(np.float16))
+    xn, _xh, _h = O.rmsnorm_rotate(conv(x), conv(w), 0.0625, np.ones((1, 128), np.float16), bf16)
+    bits = np.asarray(xn).view(np.uint16)[0]
+    assert int(bits[0]) == (0x3ED6 if bf16 else 0x36AA)
+    assert np.all(bits[1:] == (0x3FA0 if bf16 else 0x3D00))
+
+
 def test_swiglu_rotate_vs_textbook():
     rng = np.random.default_rng(2)
     rows, n = 2, 17408
