@@ -219,7 +219,11 @@ __device__ __forceinline__ uint32_t values_pos2(const uint32_t* w, uint32_t wp, 
 // provided the state register is clean (bits 16..31 zero): a shift, a bit-field extract or a byte permute
 // produces it, costing about what the window shift already cost.
 // ------------------------------------------------------------------------------------------------
-// Position P's 16-bit state in bits 0..15 of the result, zeros above.
+// Position P's 16-bit state in bits 0..15 of the result, zeros above. A window that crosses the start of word ih
+// (stream bit 32 ih) lies inside the 32 stream bits [32 ih - 16, 32 ih + 16): one funnel shift of the two words
+// by 16 serves every window crossing that boundary (the same expression, so the compiler computes it once per
+// run and boundary), and each of them is then a bit-field extract at its own offset: at K = 6, 6 funnel shifts
+// per run of 32 positions instead of 14.
 template <int K, int P>
 __device__ __forceinline__ uint32_t window_clean(const uint32_t* w, uint32_t wp) {
   using W = Win<K, P>;
@@ -230,8 +234,10 @@ __device__ __forceinline__ uint32_t window_clean(const uint32_t* w, uint32_t wp)
   } else if constexpr (W::inside) {
     return (w[W::ih] >> W::sh) & 0xFFFFu;
   } else {
+    static_assert(W::sh > 16 && W::sh < 32, "a window crossing a word boundary");
     const uint32_t prev = W::ih > 0 ? w[W::ih > 0 ? W::ih - 1 : 0] : wp;
-    return __builtin_amdgcn_alignbit(prev, w[W::ih], W::sh) & 0xFFFFu;
+    const uint32_t view = __builtin_amdgcn_alignbit(prev, w[W::ih], 16);   // stream bits [32 ih - 16, 32 ih + 16)
+    return (view >> (W::sh - 16)) & 0xFFFFu;
   }
 }
 

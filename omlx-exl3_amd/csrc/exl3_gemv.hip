@@ -53,17 +53,20 @@ constexpr int kMaxKtPerSplit = 96;
 // k-tiles per split, from the shape alone: the split never depends on the row count, so each row is summed
 // in the same order whatever the batch (row-exact results). Wide outputs (>= 128 blocks of 128 columns)
 // take 48 k-tiles: 1,000+ workgroups, several per CU, and measured at K = 6 (27B shapes) their time is flat
-// within a few percent for 40-96. Narrow outputs take as many splits as fill the chip's 256 CUs once
-// (at most 96 k-tiles each): the decode VALU work then spreads over every CU with none running two
-// workgroups. Measured at K = 6, rows 1: o_proj (40 blocks) 13.5 -> 12.0 us with 6 splits instead of 4,
-// q/k/v (64 blocks) 14.0 -> 13.1 us with 4 instead of 5 (5 puts two workgroups on a quarter of the CUs).
+// within a few percent for 24-64. Narrow outputs take as many splits as fill the chip's 256 CUs twice, when
+// that leaves a split at least 32 k-tiles, else once (at most 96 k-tiles each): every CU then runs the same
+// number of workgroups. Measured at K = 6, rows 1 (split sweeps, one k-group pair per workgroup): q/k/v
+// (64 blocks) 12.0 us at 4 splits, 11.8 at 8, 13.7 and 12.9 at 5 and 6; o_proj (40 blocks) 10.8 us at 6 splits,
+// 10.3 at 12, 11.7 at 5 and 8; down_proj (40 blocks) 18.7 us at 12, 20.3-22.8 at 8, 10, 14 and 16.
 constexpr int kSplitFillWorkgroups = 256;   // MI355X's CU count
+constexpr int kMinKtPerDoubleSplit = 32;
 static int auto_kt_per_split(int KT, int blocks) {
   const int ktr = (KT + 3) / 4 * 4;
   int kps = 48;
   if (blocks < 128) {
-    int S = kSplitFillWorkgroups / blocks;
     const int s_min = (KT + kMaxKtPerSplit - 1) / kMaxKtPerSplit;
+    int S = 2 * kSplitFillWorkgroups / blocks;
+    if ((KT + S - 1) / S < kMinKtPerDoubleSplit) S = kSplitFillWorkgroups / blocks;
     if (S < s_min) S = s_min;
     kps = ((KT + S - 1) / S + 3) / 4 * 4;
   }
