@@ -224,7 +224,9 @@ __device__ void prologue_finish(const GemvArgs& a, const ProPre& p, int kt0, int
 // workgroup serves in a gemv_kernel_mk launch. The LDS arrays are the kernel's (xs: the split's activations,
 // [(iters+WK)*4 k-tiles][rows] records + zero record; bv: the block's column sums; last: the arrival verdict;
 // ss_part / inv_rms: the prologue's per-wavefront sums of squares and inverse RMS).
-template <int K, int CB, int L, int OT>
+// PRE: activation staging units per thread loaded before the trellis prefetch (the rest after it); four in the
+// pair layout up to K = 6, two where the trellis sets (K = 7, 8) or the split layout leave no registers for more.
+template <int K, int CB, int L, int OT, int PRE = (L == kPair && K <= 6) ? 4 : 2>
 __device__ __forceinline__ void gemv_body(const GemvArgs a, u32x4* xs, float (*bv)[128], uint32_t& last,
                                           double (*ss_part)[16], float* inv_rms) {
   constexpr bool SPLIT = L == kSplit;
@@ -304,13 +306,16 @@ __device__ __forceinline__ void gemv_body(const GemvArgs a, u32x4* xs, float (*b
   const int b_split = ((kt1 + 7) >> 3) - (kt0 >> 3);
   const bool early_pro = a.pro != kProNone && rows == 1 && (a.pro != kProNorm || a.pss != nullptr) &&
                          b_split <= (nthr >> 4) && a.k / 128 <= nthr;
+  // up to PRE units per thread in flight before the trellis prefetch (with 4, all of them up to 8 rows at the
+  // 27B shapes: a unit loaded after the prefetch would return only behind two trellis sets)
+  constexpr int kPreUnits = PRE;
   ProPre pp{};
-  u32x4 pre0 = {0u, 0u, 0u, 0u}, pre1 = {0u, 0u, 0u, 0u};
+  u32x4 pre[kPreUnits];
   if (early_pro) {
     pp = prologue_preload(a, m, kt0, kt1);
   } else if (a.pro == kProNone) {
-    if (tid < nunits) pre0 = load_unit(tid);
-    if (tid + nthr < nunits) pre1 = load_unit(tid + nthr);
+#pragma unroll
+    for (int j = 0; j < kPreUnits; ++j) pre[j] = tid + j * nthr < nunits ? load_unit(tid + j * nthr) : u32x4{0u, 0u, 0u, 0u};
   }
 
   Stage<K> st[D];
@@ -326,9 +331,10 @@ __device__ __forceinline__ void gemv_body(const GemvArgs a, u32x4* xs, float (*b
   } else if (a.pro != kProNone) {
     stage_prologue<SPLIT>(a, m, blk - blk0, kt0, kt1, nrec, xs, ss_part, inv_rms);
   } else {
-    if (tid < nunits) put_unit(tid, pre0);
-    if (tid + nthr < nunits) put_unit(tid + nthr, pre1);
-    for (int idx = tid + 2 * nthr; idx < nunits; idx += nthr) put_unit(idx, load_unit(idx));
+#pragma unroll
+    for (int j = 0; j < kPreUnits; ++j)
+      if (tid + j * nthr < nunits) put_unit(tid + j * nthr, pre[j]);
+    for (int idx = tid + kPreUnits * nthr; idx < nunits; idx += nthr) put_unit(idx, load_unit(idx));
   }
   __syncthreads();
 
@@ -466,9 +472,16 @@ __device__ __forceinline__ void gemv_body(const GemvArgs a, u32x4* xs, float (*b
     __syncthreads();
     if (last == 0) return;
     load_epilogue_operands();
-    for (int idx = tid; idx < rows * 128; idx += nthr) {
-      const int r = idx >> 7, cc = idx & 127;
-      bv[r][cc] = sum_splits(part + (size_t)r * a.n_total + blk * 128 + cc, pstride, a.S);
+    // two adjacent columns per thread, split order 0..S-1 (the same sums as one column at a time)
+    const __amdgpu_buffer_rsrc_t rs_p = __builtin_amdgcn_make_buffer_rsrc(
+        part, (short)0, (int)((uint32_t)a.S * (uint32_t)pstride * 4u), kBufferFlags);
+    for (int idx = tid; idx < rows * 64; idx += nthr) {
+      const int r = idx >> 6, cc = 2 * (idx & 63);
+      float v0, v1;
+      sum_splits2_rs(rs_p, (uint32_t)((size_t)r * a.n_total + blk * 128 + cc) * 4u, (uint32_t)pstride * 4u, a.S,
+                     v0, v1);
+      bv[r][cc] = v0;
+      bv[r][cc + 1] = v1;
     }
     if (tid == 0) __hip_atomic_store(&a.counters[(size_t)blk * kCounterStride], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();

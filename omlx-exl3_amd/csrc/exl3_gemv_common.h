@@ -152,6 +152,35 @@ __device__ __forceinline__ float sum_splits(const float* src, size_t stride, int
   return v;
 }
 
+// Two adjacent columns of S split partials, as sum_splits2 below, read through a buffer descriptor over the
+// partials: lane loads of 8 bytes (both columns at once) with device-scope coherence (sc1, as the atomic loads
+// above), sixteen splits per round trip; the slots past S get an offset beyond the descriptor's range, which
+// returns zeros without touching memory (the sums add only the first S). off0: byte offset of split 0's pair,
+// stride: bytes between splits.
+__device__ __forceinline__ void sum_splits2_rs(__amdgpu_buffer_rsrc_t rs, uint32_t off0, uint32_t stride, int S,
+                                               float& v0, float& v1) {
+  constexpr int kDeviceScope = 16;   // sc1: coherent at device scope (the form a relaxed agent-scope load takes)
+  v0 = 0.f;
+  v1 = 0.f;
+  for (int s0 = 0; s0 < S; s0 += kSplitBatch) {
+    u32x2 t[kSplitBatch];
+#pragma unroll
+    for (int u = 0; u < kSplitBatch; ++u) {
+      const uint32_t off = s0 + u < S ? off0 + (uint32_t)(s0 + u) * stride : 0xFFFFFFF0u;
+      t[u] = __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, kDeviceScope);
+    }
+#pragma unroll
+    for (int u = 0; u < kSplitBatch; ++u)
+      if (s0 + u < S) {
+        // the elements as scalars first: __builtin_bit_cast of a vector element names the vector's storage,
+        // and this compiler then reads element 0 for either
+        const uint32_t e0 = t[u].x, e1 = t[u].y;
+        v0 += __builtin_bit_cast(float, e0);
+        v1 += __builtin_bit_cast(float, e1);
+      }
+  }
+}
+
 // Two adjacent columns of S split partials (src[s * stride], src[s * stride + 1]), as sum_splits.
 __device__ __forceinline__ void sum_splits2(const float* src, size_t stride, int S, float& v0, float& v1) {
   v0 = 0.f;

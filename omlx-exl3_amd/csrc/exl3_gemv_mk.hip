@@ -7,21 +7,22 @@
 
 namespace exl3 {
 
-// member m at a.Km[m] bits per weight; the workgroup's block decides its member
+// member m at a.Km[m] bits per weight; the workgroup's block decides its member. Two staging units per thread
+// go out before the trellis prefetch: with the eight bodies in one kernel, four exceed the 96-register budget.
 template <int CB, int OT>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(5))) void gemv_kernel_mk(GemvArgs a) {
   EXL3_GEMV_LDS
   const int blk = blockIdx.x;
   const int m = (blk >= a.blk_end[0]) + (blk >= a.blk_end[1]);
   switch (a.Km[m]) {
-    case 1: gemv_body<1, CB, kPair, OT>(a, xs, bv, last, ss_part, inv_rms); break;
-    case 2: gemv_body<2, CB, kPair, OT>(a, xs, bv, last, ss_part, inv_rms); break;
-    case 3: gemv_body<3, CB, kPair, OT>(a, xs, bv, last, ss_part, inv_rms); break;
-    case 4: gemv_body<4, CB, kPair, OT>(a, xs, bv, last, ss_part, inv_rms); break;
-    case 5: gemv_body<5, CB, kPair, OT>(a, xs, bv, last, ss_part, inv_rms); break;
-    case 6: gemv_body<6, CB, kPair, OT>(a, xs, bv, last, ss_part, inv_rms); break;
-    case 7: gemv_body<7, CB, kPair, OT>(a, xs, bv, last, ss_part, inv_rms); break;
-    default: gemv_body<8, CB, kPair, OT>(a, xs, bv, last, ss_part, inv_rms); break;
+    case 1: gemv_body<1, CB, kPair, OT, 2>(a, xs, bv, last, ss_part, inv_rms); break;
+    case 2: gemv_body<2, CB, kPair, OT, 2>(a, xs, bv, last, ss_part, inv_rms); break;
+    case 3: gemv_body<3, CB, kPair, OT, 2>(a, xs, bv, last, ss_part, inv_rms); break;
+    case 4: gemv_body<4, CB, kPair, OT, 2>(a, xs, bv, last, ss_part, inv_rms); break;
+    case 5: gemv_body<5, CB, kPair, OT, 2>(a, xs, bv, last, ss_part, inv_rms); break;
+    case 6: gemv_body<6, CB, kPair, OT, 2>(a, xs, bv, last, ss_part, inv_rms); break;
+    case 7: gemv_body<7, CB, kPair, OT, 2>(a, xs, bv, last, ss_part, inv_rms); break;
+    default: gemv_body<8, CB, kPair, OT, 2>(a, xs, bv, last, ss_part, inv_rms); break;
   }
 }
 
