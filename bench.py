@@ -248,11 +248,19 @@ def mixed_k_benchmark(pk, torch, dev, rows_list=(1, 2, 4, 8), n_layers=8, reps=1
 
     def whole(items, nbytes):
         graph = graph_of(items)
-        ms = time_graph(graph)
+        ms = statistics.median(time_graph(graph) for _ in range(3))
         del graph
         return {"launches_per_layer": round(len(items) / n_layers, 2), "us_per_layer": round(ms * 1e3 / n_layers, 1),
                 "GB_s": round(nbytes / ms / 1e6, 1), "pct_hbm_peak": round(100 * nbytes / ms / 1e6 / HBM_PEAK_GBS, 1)}
 
+    # warm-up: the first form's graph replayed ~100 times before any timing (the clocks settle under load;
+    # without it the first form measured, rows 1, read up to 10% slow)
+    items, _nb = launches(rows_list[0], by_k=False)
+    gr = graph_of(items)
+    for _ in range(100):
+        gr.replay()
+    torch.cuda.synchronize()
+    del gr, items
     for rows in rows_list:
         items, nbytes = launches(rows, by_k=False)
         res = whole(items, nbytes)
@@ -264,7 +272,7 @@ def mixed_k_benchmark(pk, torch, dev, rows_list=(1, 2, 4, 8), n_layers=8, reps=1
         for K in sorted({plan.K for plan, _x, _t, _o in items}):
             sel = [it for it in items if it[0].K == K]
             gr = graph_of(sel)
-            ms_k = time_graph(gr)
+            ms_k = statistics.median(time_graph(gr) for _ in range(3))
             del gr
             nb = sum(algorithmic_bytes(p.k, p.ns, p.K, rows) for p, _x, _t, _o in sel)
             per_k[str(K)] = {"launches": len(sel), "GB_s": round(nb / ms_k / 1e6, 1),

@@ -1,12 +1,11 @@
 // SPDX-License-Identifier: Apache-2.0
-// Output rotation for a prefill whose GEMM runs in the caller's BLAS library (the package's "library"
-// comparison form): y = had128(g) * svh (+ bias) for a (rows, n) fp16 product g. That form is built as the
-// reference's prefill is (src/omlx/exl3/linear.py:97-105: decode_wt to fp16 weights, an fp16 matmul,
-// hadamard_transform, svh): exl3_reconstruct writes W_inner^T once, the host multiplies with the process's
-// BLAS library (hipBLASLt through PyTorch; linking this library against the system hipBLASLt would bind it, by
-// soname, to the different hipBLASLt build PyTorch has already loaded), and this kernel applies the 128-point
-// Hadamard transform of each 128-column block, 1/sqrt(128), svh and bias. The default prefill
-// (exl3_prefill_mm.hip) does the GEMM and this rotation in one hand-written launch.
+// Output rotation for a prefill whose GEMM runs elsewhere (bench.py's comparison leg multiplies with hipBLASLt
+// through PyTorch): y = had128(g) * svh (+ bias) for a (rows, n) fp16 product g, i.e. the reference's prefill
+// structure (src/omlx/exl3/linear.py:97-105: decode_wt to fp16 weights, an fp16 matmul, hadamard_transform, svh)
+// after exl3_reconstruct and any GEMM: the 128-point Hadamard transform of each 128-column block, 1/sqrt(128),
+// svh and bias. The package's prefill (exl3_prefill_mm.hip) does the GEMM and this rotation in one hand-written
+// launch. (This library links no BLAS: linked against the system hipBLASLt it would bind, by soname, to the
+// different hipBLASLt build PyTorch has already loaded.)
 #include "exl3_capi_common.h"
 #include "exl3_device.h"
 
