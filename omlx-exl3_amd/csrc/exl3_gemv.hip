@@ -270,6 +270,8 @@ static int gemv_run(const uint16_t* xh, const GemvPrologueArgs& pro, const uint3
   const int layout = mixed ? kPair : layout_for(cb, flags);
   const int kps = kt_per_split > 0 ? ((kt_per_split + 3) / 4) * 4 : auto_kt_per_split(KT, blocks);
   const int S = (KT + kps - 1) / kps;
+  // every split starts inside k and holds at least one k-tile (its trellis descriptor's range is nkt rows)
+  EXL3_REQUIRE(kps > 0 && (S - 1) * kps < KT, EXL3_ERR_ARG, "exl3_gemv: split of %d k-tiles leaves an empty split", kps);
   const int WK = auto_k_groups(blocks, S);
   // staged activations: ((iters + WK) * 4 * rows + 1) records of 32 bytes (64 in the split layout)
   const size_t smem = ((size_t)(kps / 4 + WK) * 4 * rows + 1) * (layout == kSplit ? 64 : 32);
