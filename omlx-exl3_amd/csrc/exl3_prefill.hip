@@ -108,7 +108,8 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const uint16_t* __r
 
   // ---------------- pipeline ----------------
   uint32_t w0[K], w1[K], wp0 = 0, wp1 = 0;   // decode: words of steps s+1 (w0) and s+2 (w1)
-  u32x4 Aring[3][4];                          // A fragments of slices g, g+1, g+2
+  constexpr int kRingA = 4, kRingB = 5;       // A: slices g .. g+3 (three ahead); B: fragments f .. f+4
+  u32x4 Aring[kRingA][4];
   if (decoder) {
     uint32_t w[K], wp;
     load_run_words(0, w, wp);
@@ -119,17 +120,18 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const uint16_t* __r
     // zero weights (step 1 lies past the matrix) so that LDS left over from earlier kernels is never read
     if (nsteps == 1) store_run(1, 1, w, wp);
   } else {
-    load_A(0, Aring[0]);
-    load_A(1, Aring[1]);
+#pragma unroll
+    for (int g = 0; g < kRingA - 1; ++g) load_A(g, Aring[g]);
   }
   __syncthreads();
 
   // The two roles run separate loops with one barrier per step each (same count), so the compiler's wait
-  // analysis of one role never sees the other role's loads. The step count is padded to a multiple of three
+  // analysis of one role never sees the other role's loads. The step count is padded to a multiple of two
   // (the MFMA loop's unroll): padded steps decode nothing and contract zero activations (k past the matrix
   // reads zeros) with finite weights in LDS (an earlier step's, or the zeros written above), adding exactly
   // zero.
-  const int nsteps_pad = (nsteps + 2) / 3 * 3;
+  constexpr int kStepsPerGroup = kRingA / 2;
+  const int nsteps_pad = (nsteps + kStepsPerGroup - 1) / kStepsPerGroup * kStepsPerGroup;
   if (decoder) {
     for (int s = 0; s < nsteps_pad; ++s) {
       if (s + 1 < nsteps) {
@@ -147,31 +149,33 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const uint16_t* __r
     }
     return;
   }
-  // MFMA role: steps in groups of three so that the six slices of a group use the A ring slots at
-  // compile-time indices (slice g in slot g % 3): no register copies, so no wait on loads still in flight.
-  // Within a step, the 16 weight fragments (2 slices x 8 column tiles) are read through a ring of three,
-  // two fragments ahead of the MFMAs that use them; scheduling barriers keep that order, so LDS latency
-  // hides behind matrix work instead of stalling it.
+  // MFMA role: steps in groups of two so that the four slices of a group use the A ring slots at
+  // compile-time indices (slice g in slot g % 4, loaded three slices ahead): no register copies, so no wait
+  // on loads still in flight. Within a step, the 16 weight fragments (2 slices x 8 column tiles) are read
+  // through a ring of five, four fragments ahead of the MFMAs that use them (an LDS read's latency is several
+  // MFMAs long); scheduling barriers keep that order, so LDS latency hides behind matrix work instead of
+  // stalling it.
   const uint16_t* bbase = sB[0] + c * kPfLdB + 8 * q;
   constexpr int kBufHalves = 128 * kPfLdB;
   auto read_B = [&](int buf, int f) {
     return *reinterpret_cast<const u32x4*>(bbase + buf * kBufHalves + ((f & 7) * 16) * kPfLdB + (f >> 3) * 32);
   };
-  for (int s0 = 0; s0 < nsteps_pad; s0 += 3) {
-    static_for<0, 3>([&](auto D) {
+  for (int s0 = 0; s0 < nsteps_pad; s0 += kStepsPerGroup) {
+    static_for<0, kStepsPerGroup>([&](auto D) {
       constexpr int d = decltype(D)::value;
       const int s = s0 + d;
       const int buf = s & 1;
-      u32x4 Bring[3];
-      Bring[0] = read_B(buf, 0);
-      Bring[1] = read_B(buf, 1);
+      u32x4 Bring[kRingB];
+#pragma unroll
+      for (int f = 0; f < kRingB - 1; ++f) Bring[f] = read_B(buf, f);
       static_for<0, 16>([&](auto F) {
         constexpr int f = decltype(F)::value;
         constexpr int sl = f >> 3, j = f & 7;
-        constexpr int slot = (2 * d + sl) % 3;
-        if constexpr (j == 0) load_A(2 * s + sl + 2, Aring[(2 * d + sl + 2) % 3]);   // past the end: zeros
-        if constexpr (f + 2 < 16) Bring[(f + 2) % 3] = read_B(buf, f + 2);
-        const f16x8 B = __builtin_bit_cast(f16x8, Bring[f % 3]);
+        constexpr int slot = (2 * d + sl) % kRingA;
+        if constexpr (j == 0)   // slice 2 s + sl + 3 (past the end: zeros) into the slot slice 2 s + sl - 1 used
+          load_A(2 * s + sl + kRingA - 1, Aring[(2 * d + sl + kRingA - 1) % kRingA]);
+        if constexpr (f + kRingB - 1 < 16) Bring[(f + kRingB - 1) % kRingB] = read_B(buf, f + kRingB - 1);
+        const f16x8 B = __builtin_bit_cast(f16x8, Bring[f % kRingB]);
 #pragma unroll
         for (int i = 0; i < 4; ++i)
           acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, Aring[slot][i]), B, acc[i][j],
