@@ -46,20 +46,17 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const uint16_t* __r
   // lane's run in each step: k-tile (t >> 6) of the step, n-tile ((t >> 3) & 7), run g = t & 7
   const int t = tid & 255;
   const int r_kt = t >> 6, r_nt = (t >> 3) & 7, r_g = t & 7;
-  const uint32_t* trun = tr + ((size_t)r_kt * NT + nb * 8 + r_nt) * TW;   // + step * 4 * NT * TW
-  const size_t tstep = (size_t)4 * NT * TW;
-  const int wofs = K * r_g, wpofs = (K * r_g + TW - 1) % TW;
+  // the trellis through a buffer descriptor (k n K / 8 bytes, below 2 GiB: checked on the host): a run past the
+  // matrix gets an offset past the descriptor and reads zeros, so the loads carry no branch and no register
+  // writes besides their own
+  const __amdgpu_buffer_rsrc_t rs_tr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint32_t*>(tr), (short)0, (int)((uint32_t)KT * (uint32_t)NT * (uint32_t)TW * 4u), kBufferFlags);
+  const uint32_t run_bytes = (uint32_t)((r_kt * NT + nb * 8 + r_nt) * TW) * 4u;   // + step * tstep_bytes
+  const uint32_t tstep_bytes = 4u * (uint32_t)NT * (uint32_t)TW * 4u;
+  const uint32_t wofs = 4u * (uint32_t)(K * r_g), wpofs = 4u * (uint32_t)((K * r_g + TW - 1) % TW);
   auto load_run_words = [&](int s, uint32_t* w, uint32_t& wp) {
-    if (s < nsteps && s * 4 + r_kt < KT) {
-      const uint32_t* tp = trun + (size_t)s * tstep;
-#pragma unroll
-      for (int i = 0; i < K; ++i) w[i] = tp[wofs + i];
-      wp = tp[wpofs];
-    } else {
-#pragma unroll
-      for (int i = 0; i < K; ++i) w[i] = 0u;
-      wp = 0u;
-    }
+    const uint32_t base = s * 4 + r_kt < KT ? run_bytes + (uint32_t)s * tstep_bytes : 0x80000000u;
+    load_run<K>(rs_tr, base + wofs, base + wpofs, 0u, w, wp);
   };
   // decoded run -> LDS: column g (lo) and 8 + g (hi) of n-tile r_nt, k 16 r_kt .. 16 r_kt + 15
   auto store_run = [&](int buf, int s, const uint32_t* w, uint32_t wp) {
@@ -107,14 +104,17 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const uint16_t* __r
     for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   // ---------------- pipeline ----------------
-  uint32_t w0[K], w1[K], wp0 = 0, wp1 = 0;   // decode: words of steps s+1 (w0) and s+2 (w1)
+  // decode: two word sets used in turn, X for the odd steps (decoded at even s), Y for the even ones; each is
+  // decoded and then reloaded for the step two later, so a set's loads have two steps to land and no register
+  // copy ever waits on a load in flight
+  uint32_t wX[K], wY[K], wpX = 0, wpY = 0;
   constexpr int kRingA = 4, kRingB = 5;       // A: slices g .. g+3 (three ahead); B: fragments f .. f+4
   u32x4 Aring[kRingA][4];
   if (decoder) {
     uint32_t w[K], wp;
     load_run_words(0, w, wp);
-    load_run_words(1, w0, wp0);
-    load_run_words(2, w1, wp1);
+    load_run_words(1, wX, wpX);
+    load_run_words(2, wY, wpY);
     store_run(0, 0, w, wp);
     // one k-step (k <= 64): the padded steps also read the second half, which no step writes; fill it with
     // zero weights (step 1 lies past the matrix) so that LDS left over from earlier kernels is never read
@@ -133,18 +133,13 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const uint16_t* __r
   constexpr int kStepsPerGroup = kRingA / 2;
   const int nsteps_pad = (nsteps + kStepsPerGroup - 1) / kStepsPerGroup * kStepsPerGroup;
   if (decoder) {
-    for (int s = 0; s < nsteps_pad; ++s) {
-      if (s + 1 < nsteps) {
-        uint32_t w[K], wp;
-#pragma unroll
-        for (int i = 0; i < K; ++i) w[i] = w0[i];
-        wp = wp0;
-#pragma unroll
-        for (int i = 0; i < K; ++i) w0[i] = w1[i];
-        wp0 = wp1;
-        load_run_words(s + 3, w1, wp1);
-        store_run((s + 1) & 1, s + 1, w, wp);
-      }
+    static_assert(kStepsPerGroup == 2, "the decode loop takes its two word sets in turn, one step each");
+    for (int s = 0; s < nsteps_pad; s += 2) {
+      if (s + 1 < nsteps) store_run(1, s + 1, wX, wpX);   // step s + 1 into half (s + 1) & 1
+      load_run_words(s + 3, wX, wpX);                      // past the matrix: zeros, nothing loaded
+      __syncthreads();
+      if (s + 2 < nsteps) store_run(0, s + 2, wY, wpY);
+      load_run_words(s + 4, wY, wpY);
       __syncthreads();
     }
     return;
@@ -268,6 +263,8 @@ extern "C" int exl3_prefill_gemm(const uint16_t* xh, const uint32_t* trellis, in
   EXL3_REQUIRE((rows + kPfBM - 1) / kPfBM <= 65535, EXL3_ERR_ARG, "exl3_prefill_gemm: too many rows");
   EXL3_REQUIRE((uint64_t)rows * (uint64_t)k * 2u < (1ull << 31), EXL3_ERR_ARG,
                "exl3_prefill_gemm: activations exceed 2 GiB (rows x k)");
+  EXL3_REQUIRE((uint64_t)k * (uint64_t)n * (uint64_t)K / 8u < (1ull << 31), EXL3_ERR_ARG,
+               "exl3_prefill_gemm: trellis exceeds 2 GiB (k x n x K / 8 bytes)");
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (K) {
     case 1: launch_prefill_cb<1>(cb, out_dtype, xh, trellis, k, n, rows, svh, bias, y, st); break;
