@@ -475,11 +475,24 @@ __device__ __forceinline__ void gemv_body(const GemvArgs a, u32x4* xs, float (*b
     // two adjacent columns per thread, split order 0..S-1 (the same sums as one column at a time)
     const __amdgpu_buffer_rsrc_t rs_p = __builtin_amdgcn_make_buffer_rsrc(
         part, (short)0, (int)((uint32_t)a.S * (uint32_t)pstride * 4u), kBufferFlags);
-    for (int idx = tid; idx < rows * 64; idx += nthr) {
+    auto pair_off = [&](int idx) { return (uint32_t)((size_t)(idx >> 6) * a.n_total + blk * 128 + 2 * (idx & 63)) * 4u; };
+    int idx = tid;
+    // two pairs per thread while there are (more pairs than threads: the wide launch's 256 threads from 5 rows),
+    // their loads in one round trip
+    if (a.S <= kSplitBatch / 2) {
+      for (; idx + nthr < rows * 64; idx += 2 * nthr) {
+        float v0, v1, w0, w1;
+        sum_splits2x2_rs(rs_p, pair_off(idx), pair_off(idx + nthr), (uint32_t)pstride * 4u, a.S, v0, v1, w0, w1);
+        bv[idx >> 6][2 * (idx & 63)] = v0;
+        bv[idx >> 6][2 * (idx & 63) + 1] = v1;
+        bv[(idx + nthr) >> 6][2 * ((idx + nthr) & 63)] = w0;
+        bv[(idx + nthr) >> 6][2 * ((idx + nthr) & 63) + 1] = w1;
+      }
+    }
+    for (; idx < rows * 64; idx += nthr) {
       const int r = idx >> 6, cc = 2 * (idx & 63);
       float v0, v1;
-      sum_splits2_rs(rs_p, (uint32_t)((size_t)r * a.n_total + blk * 128 + cc) * 4u, (uint32_t)pstride * 4u, a.S,
-                     v0, v1);
+      sum_splits2_rs(rs_p, pair_off(idx), (uint32_t)pstride * 4u, a.S, v0, v1);
       bv[r][cc] = v0;
       bv[r][cc + 1] = v1;
     }

@@ -181,6 +181,30 @@ __device__ __forceinline__ void sum_splits2_rs(__amdgpu_buffer_rsrc_t rs, uint32
   }
 }
 
+// Two column pairs at once (offsets offA, offB), S <= kSplitBatch / 2: all 2 S loads in one round trip, each pair
+// summed in split order as sum_splits2_rs does (the same values).
+__device__ __forceinline__ void sum_splits2x2_rs(__amdgpu_buffer_rsrc_t rs, uint32_t offA, uint32_t offB,
+                                                 uint32_t stride, int S, float& a0, float& a1, float& b0,
+                                                 float& b1) {
+  constexpr int kDeviceScope = 16;   // sc1: coherent at device scope (the form a relaxed agent-scope load takes)
+  constexpr int H = kSplitBatch / 2;
+  u32x2 ta[H], tb[H];
+#pragma unroll
+  for (int u = 0; u < H; ++u) ta[u] = __builtin_amdgcn_raw_buffer_load_b64(rs, u < S ? offA + (uint32_t)u * stride : 0xFFFFFFF0u, 0, kDeviceScope);
+#pragma unroll
+  for (int u = 0; u < H; ++u) tb[u] = __builtin_amdgcn_raw_buffer_load_b64(rs, u < S ? offB + (uint32_t)u * stride : 0xFFFFFFF0u, 0, kDeviceScope);
+  a0 = a1 = b0 = b1 = 0.f;
+#pragma unroll
+  for (int u = 0; u < H; ++u)
+    if (u < S) {
+      const uint32_t e0 = ta[u].x, e1 = ta[u].y, f0 = tb[u].x, f1 = tb[u].y;
+      a0 += __builtin_bit_cast(float, e0);
+      a1 += __builtin_bit_cast(float, e1);
+      b0 += __builtin_bit_cast(float, f0);
+      b1 += __builtin_bit_cast(float, f1);
+    }
+}
+
 // Two adjacent columns of S split partials (src[s * stride], src[s * stride + 1]), as sum_splits.
 __device__ __forceinline__ void sum_splits2(const float* src, size_t stride, int S, float& v0, float& v1) {
   v0 = 0.f;
