@@ -231,10 +231,12 @@ def test_gemv_27b_shapes_vs_reconstruct(pk, name):
 
 
 @pytest.mark.parametrize("name,K,rows", [("qkv", 3, 4), ("o", 8, 2), ("gate_up", 2, 4), ("down", 5, 2),
-                                         ("gate_up", 4, 8), ("kv", 8, 1), ("q", 2, 2)])
+                                         ("gate_up", 4, 8), ("kv", 8, 1), ("q", 2, 2), ("gate_up", 5, 5),
+                                         ("gate_up", 3, 16)])
 def test_gemv_27b_shapes_mixed_bitrates(pk, name, K, rows):
     """Config 3's cases: full-size 27B projections at the other per-tensor bitrates {2, 3, 4, 5, 8} and batch
-    rows 1, 2, 4 and 8, against had128(xh @ W) * svh with W from the bit-exact reconstruct kernel and an fp32
+    rows 1, 2, 4 and 8 (and 5 and 16 on the wide launch, whose last arriver reloads two column pairs per thread
+    from 5 rows on), against had128(xh @ W) * svh with W from the bit-exact reconstruct kernel and an fp32
     matmul; row 0 equals the single-row result bit for bit."""
     k, ns = SHAPES_27B[name]
     g = torch.Generator(device="cuda").manual_seed(100 * K + rows)
