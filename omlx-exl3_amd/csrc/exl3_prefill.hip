@@ -10,11 +10,12 @@
 //   decode wavefronts (4-7): one trellis run per lane per step (4 k-tiles x 8 n-tiles x 8 runs = 256 runs),
 //     prefetched two steps ahead, decoded into the next step's half of a double-buffered LDS weight tile
 //     (n-major, 16-byte pair groups, the B-operand layout of v_mfma_f32_16x16x32_f16);
-//   MFMA wavefronts (0-3): 64 rows each; activations loaded straight into A-operand registers two 32-k
-//     slices ahead (a ring of three; rows past the batch read zero through the buffer descriptor), 64 MFMAs
-//     per step against the current half of the weight tile.
-// One barrier per step hands the tile halves over, so decoding (VALU) overlaps the matrix work (MFMA) on
-// the same SIMDs. Epilogue: the 128-point FWHT of each row runs in registers (stages 1, 2, 4, 8 across the 16
+//   MFMA wavefronts (0-3): 64 rows each; the tile's activations for the next step loaded from xh straight into
+//     the other half of a double-buffered LDS tile (buffer loads with an LDS destination; rows past the batch
+//     and k past the row read zero through the buffer descriptor), A and B fragments read from LDS, 64 MFMAs
+//     per step against the current halves.
+// One barrier per step hands the halves over, so decoding (VALU) overlaps the matrix work (MFMA) on the same
+// SIMDs. Epilogue: the 128-point FWHT of each row runs in registers (stages 1, 2, 4, 8 across the 16
 // lanes of a column group, 16, 32, 64 across the accumulator tiles of a lane), then 1/sqrt(128), svh, bias.
 #include "exl3_capi_common.h"
 #include "exl3_device.h"
@@ -34,8 +35,14 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const uint16_t* __r
                                                              const void* __restrict__ bias, void* __restrict__ y) {
   constexpr int TW = 8 * K;
   __shared__ __attribute__((aligned(16))) uint16_t sB[2][128 * kPfLdB];
+  // the two activation stages as separate arrays: with the stage of each access known at compile time, the
+  // compiler sees that the loads into one stage do not touch the fragments read from the other (and waits for
+  // none of them before an LDS read)
+  __shared__ u32x4 sA0[kPfBM * 8], sA1[kPfBM * 8];
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  // (wave through readfirstlane: uniform, so the LDS destinations of the activation loads, which go to M0, are
+  // computed in scalar registers)
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int nb = blockIdx.x;                 // 128-column block
   const int row0 = blockIdx.y * kPfBM;
   const int KT = k / 16, NT = n / 16;
@@ -80,22 +87,32 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const uint16_t* __r
   // ---------------- MFMA role ----------------
   // lane (16q + c): A rows 16 i + c of this wavefront's 64, k 8q .. 8q+7 of each 32-k slice
   const int q = lane >> 4, c = lane & 15;
-  const int wrow0 = row0 + wave * 64;
   const __amdgpu_buffer_rsrc_t rs_x = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(xh), (short)0, (int)((uint32_t)rows * (uint32_t)k * 2u), kBufferFlags);
-  // A fragments of 32-k slice `g` (= step g / 2, half g % 2) for the 4 row tiles
-  // Rows past the batch and k past the row get an offset past the descriptor, so the load itself returns
-  // zeros (selecting the address, not the loaded value, keeps the load a prefetch: nothing waits for it).
-  const uint32_t oob = (uint32_t)rows * (uint32_t)k * 2u;
-  auto load_A = [&](int g, u32x4 (&A)[4]) {
-    const int kk = g * 32 + 8 * q;
+  // Activations: a step's 256 rows x 64 k (32 KiB) go from xh straight into one of two LDS stages (buffer loads
+  // with an LDS destination, no registers), issued by the MFMA wavefronts a step ahead. Lane L of wavefront w's j-th
+  // load fills slot (8 w + j) 64 + L: row (8 w + j) 8 + L / 8 of the tile at position L % 8, which holds the 8 k
+  // at piece (L % 8) ^ (row & 7) (each row is 8 pieces of 16 bytes; with this placement the fragment reads, one
+  // piece of 16 consecutive rows, and the 1 KiB load runs are free of LDS bank conflicts). Rows past the batch,
+  // pieces past k and steps past the matrix get an offset past the descriptor and read zeros, so a step beyond
+  // k contracts zeros with whatever weights the LDS holds.
+  const int arow = lane >> 3;
+  const int apos8 = ((lane & 7) ^ (arow & 7)) * 8;   // the k offset of this lane's piece (row & 7 = arow & 7)
+  uint32_t abase[8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = wrow0 + 16 * i + c;
-      const uint32_t off = (r < rows && kk < k) ? (uint32_t)r * (uint32_t)k * 2u + (uint32_t)kk * 2u : oob;
-      A[i] = __builtin_amdgcn_raw_buffer_load_b128(rs_x, off, 0u, 0);
-    }
+  for (int j = 0; j < 8; ++j) {
+    const int r = row0 + (wave * 8 + j) * 8 + arow;
+    abase[j] = r < rows ? ((uint32_t)r * (uint32_t)k + (uint32_t)apos8) * 2u : 0x80000000u;
+  }
+  // load j of step s into a stage (the builtin's pointer and offset go through plain local variables)
+  auto issue_A = [&](int s, u32x4* stage, int j) {
+    u32x4* dst = stage + (wave * 8 + j) * 64;
+    uint32_t vo = (s < nsteps && apos8 < k - 64 * s) ? abase[j] + (uint32_t)s * 128u : 0x80000000u;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_x, dst, 16, vo, 0, 0, 0);
   };
+  // fragment of row tile i, 32-k slice sl: row 64 w + 16 i + c, piece 4 sl + q
+  const int afrag = (wave * 64 + c) * 8;
+  auto read_A = [&](const u32x4* stage, int i, int sl) { return stage[afrag + i * 128 + ((4 * sl + q) ^ (c & 7))]; };
 
   f32x4 acc[4][8];
 #pragma unroll
@@ -108,8 +125,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const uint16_t* __r
   // decoded and then reloaded for the step two later, so a set's loads have two steps to land and no register
   // copy ever waits on a load in flight
   uint32_t wX[K], wY[K], wpX = 0, wpY = 0;
-  constexpr int kRingA = 4, kRingB = 5;       // A: slices g .. g+3 (three ahead); B: fragments f .. f+4
-  u32x4 Aring[kRingA][4];
+  constexpr int kRingB = 5;   // B: fragments f .. f+4
   if (decoder) {
     uint32_t w[K], wp;
     load_run_words(0, w, wp);
@@ -120,8 +136,10 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const uint16_t* __r
     // zero weights (step 1 lies past the matrix) so that LDS left over from earlier kernels is never read
     if (nsteps == 1) store_run(1, 1, w, wp);
   } else {
+    // step 0 into stage 0, landed before the barrier
 #pragma unroll
-    for (int g = 0; g < kRingA - 1; ++g) load_A(g, Aring[g]);
+    for (int j = 0; j < 8; ++j) issue_A(0, sA0, j);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
   __syncthreads();
 
@@ -130,7 +148,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const uint16_t* __r
   // (the MFMA loop's unroll): padded steps decode nothing and contract zero activations (k past the matrix
   // reads zeros) with finite weights in LDS (an earlier step's, or the zeros written above), adding exactly
   // zero.
-  constexpr int kStepsPerGroup = kRingA / 2;
+  constexpr int kStepsPerGroup = 2;
   const int nsteps_pad = (nsteps + kStepsPerGroup - 1) / kStepsPerGroup * kStepsPerGroup;
   if (decoder) {
     static_assert(kStepsPerGroup == 2, "the decode loop takes its two word sets in turn, one step each");
@@ -144,42 +162,53 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const uint16_t* __r
     }
     return;
   }
-  // MFMA role: steps in groups of two so that the four slices of a group use the A ring slots at
-  // compile-time indices (slice g in slot g % 4, loaded three slices ahead): no register copies, so no wait
-  // on loads still in flight. Within a step, the 16 weight fragments (2 slices x 8 column tiles) are read
-  // through a ring of five, four fragments ahead of the MFMAs that use them (an LDS read's latency is several
-  // MFMAs long); scheduling barriers keep that order, so LDS latency hides behind matrix work instead of
-  // stalling it.
+  // MFMA role: step s reads its activations from stage s % 2 and issues step s + 1's into the other stage (read
+  // last in step s - 1), one load per group of four MFMAs over the first half of the step; they have landed
+  // before the step's closing barrier. Within a step, the 16 weight fragments (2 slices x 8 column tiles) are
+  // read through a ring of five, four fragments ahead of the MFMAs that use them, and the second slice's
+  // activation fragments half a slice ahead (an LDS read's latency is several MFMAs long); scheduling barriers
+  // keep that order, so LDS latency hides behind matrix work instead of stalling it. (Activations fetched two
+  // steps ahead through a third stage were level; fetched by each lane into registers, 12% slower.)
   const uint16_t* bbase = sB[0] + c * kPfLdB + 8 * q;
   constexpr int kBufHalves = 128 * kPfLdB;
   auto read_B = [&](int buf, int f) {
     return *reinterpret_cast<const u32x4*>(bbase + buf * kBufHalves + ((f & 7) * 16) * kPfLdB + (f >> 3) * 32);
   };
-  for (int s0 = 0; s0 < nsteps_pad; s0 += kStepsPerGroup) {
-    static_for<0, kStepsPerGroup>([&](auto D) {
-      constexpr int d = decltype(D)::value;
-      const int s = s0 + d;
-      const int buf = s & 1;
-      u32x4 Bring[kRingB];
+  auto mfma_step = [&](int s, const u32x4* a_cur, u32x4* a_next) {
+    const int buf = s & 1;
+    u32x4 Af[2][4];
 #pragma unroll
-      for (int f = 0; f < kRingB - 1; ++f) Bring[f] = read_B(buf, f);
-      static_for<0, 16>([&](auto F) {
-        constexpr int f = decltype(F)::value;
-        constexpr int sl = f >> 3, j = f & 7;
-        constexpr int slot = (2 * d + sl) % kRingA;
-        if constexpr (j == 0)   // slice 2 s + sl + 3 (past the end: zeros) into the slot slice 2 s + sl - 1 used
-          load_A(2 * s + sl + kRingA - 1, Aring[(2 * d + sl + kRingA - 1) % kRingA]);
-        if constexpr (f + kRingB - 1 < 16) Bring[(f + kRingB - 1) % kRingB] = read_B(buf, f + kRingB - 1);
-        const f16x8 B = __builtin_bit_cast(f16x8, Bring[f % kRingB]);
+    for (int i = 0; i < 4; ++i) Af[0][i] = read_A(a_cur, i, 0);
+    u32x4 Bring[kRingB];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, Aring[slot][i]), B, acc[i][j],
-                                                             0, 0, 0);
-        __builtin_amdgcn_sched_barrier(0);
-      });
-      __syncthreads();
+    for (int f = 0; f < kRingB - 1; ++f) Bring[f] = read_B(buf, f);
+    static_for<0, 16>([&](auto F) {
+      constexpr int f = decltype(F)::value;
+      constexpr int sl = f >> 3, j = f & 7;
+      if constexpr (f < 8) issue_A(s + 1, a_next, f);   // past the matrix: zeros
+      if constexpr (f == 4) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) Af[1][i] = read_A(a_cur, i, 1);
+      }
+      if constexpr (f + kRingB - 1 < 16) Bring[(f + kRingB - 1) % kRingB] = read_B(buf, f + kRingB - 1);
+      const f16x8 B = __builtin_bit_cast(f16x8, Bring[f % kRingB]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, Af[sl][i]), B, acc[i][j],
+                                                           0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
     });
+    // step s + 1's activations have landed in LDS before any wavefront goes on
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+  };
+  // two steps per trip (nsteps_pad is even), so that each step's stages are known at compile time
+  for (int s0 = 0; s0 < nsteps_pad; s0 += kStepsPerGroup) {
+    mfma_step(s0, sA0, sA1);
+    mfma_step(s0 + 1, sA1, sA0);
   }
+  // no LDS-bound load is left in flight when the workgroup ends
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   // ---------------- epilogue (MFMA wavefronts) ----------------
   // acc[i][j][r] = row 16 i + 4 q + r, column 16 j + c of the tile; FWHT over the 128 columns of each row:
@@ -214,7 +243,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const uint16_t* __r
           }
         }
       }
-      const int gr = wrow0 + 16 * i + 4 * q + r;
+      const int gr = row0 + wave * 64 + 16 * i + 4 * q + r;
       if (gr < rows) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
