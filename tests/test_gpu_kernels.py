@@ -655,3 +655,29 @@ def test_prefill_row_count_edges(pk, rows, path):
     ref = O.gemv_ref(xh, O.reconstruct_inner(tr, k, n, K, 0), svh)
     y = pk.kernels.prefill_gemm(dev(xh), dev(tr), k, n, K, 0, dev(svh), out_dtype=torch.float32, path=path)
     assert O.max_abs_rel(y.cpu().numpy(), ref) < 2e-3
+
+
+@pytest.mark.parametrize("k,rows", [(80, 300), (208, 1), (1040, 257), (16, 40)])
+def test_prefill_fused_k_not_multiple_of_64(pk, k, rows):
+    """k a multiple of 16 but not of 64 goes through the fused form (`auto` picks it, the matmul form needs
+    k % 64 == 0): its last k-step is partial, so the activation pieces past k and the weight tiles past the
+    last k-tile must contribute nothing. Against the oracle, `auto` equal to `fused`, and a row of infinities
+    stays in its own row (the pieces past k of the row before it read zeros, not its neighbour's data)."""
+    n, K = 256, 5
+    rng = np.random.default_rng(k + rows)
+    tr = O.random_trellis(k, n, K, 5)
+    svh = (rng.standard_normal(n) * 0.05).astype(np.float16)
+    xh = rng.standard_normal((rows, k)).astype(np.float16)
+    ref = O.gemv_ref(xh, O.reconstruct_inner(tr, k, n, K, 0), svh)
+    y = pk.kernels.prefill_gemm(dev(xh), dev(tr), k, n, K, 0, dev(svh), out_dtype=torch.float32, path="fused")
+    assert O.max_abs_rel(y.cpu().numpy(), ref) < 2e-3
+    ya = pk.kernels.prefill_gemm(dev(xh), dev(tr), k, n, K, 0, dev(svh), out_dtype=torch.float32, path="auto")
+    assert torch.equal(ya, y)
+    if rows > 2:
+        xi = xh.copy()
+        xi[1] = np.inf
+        yi = pk.kernels.prefill_gemm(dev(xi), dev(tr), k, n, K, 0, dev(svh), out_dtype=torch.float32,
+                                     path="fused").cpu()
+        keep = [r for r in range(rows) if r != 1]
+        assert torch.isfinite(yi[keep]).all()
+        assert torch.equal(yi[keep], y.cpu()[keep])
