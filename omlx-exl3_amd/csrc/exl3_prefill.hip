@@ -6,14 +6,14 @@
 // with fp32 accumulation; the 128-column output tile is one Hadamard block, so the output rotation, svh and
 // bias are applied in the epilogue.
 //
-// Workgroup = 512 threads, tile = 256 rows x 128 columns, k advances 64 per step, in two roles:
-//   decode wavefronts (4-7): one trellis run per lane per step (4 k-tiles x 8 n-tiles x 8 runs = 256 runs),
+// Workgroup = 768 threads, tile = 256 rows x 128 columns, k advances 64 per step, in two roles:
+//   decode wavefronts (8-11, one per SIMD): one trellis run per lane per step (4 k-tiles x 8 n-tiles x 8 runs = 256 runs),
 //     prefetched two steps ahead, decoded into the next step's half of a double-buffered LDS weight tile
 //     (n-major, 16-byte pair groups, the B-operand layout of v_mfma_f32_16x16x32_f16);
-//   MFMA wavefronts (0-3): 64 rows each; the tile's activations for the next step loaded from xh straight into
-//     the other half of a double-buffered LDS tile (buffer loads with an LDS destination; rows past the batch
-//     and k past the row read zero through the buffer descriptor), A and B fragments read from LDS, 64 MFMAs
-//     per step against the current halves.
+//   MFMA wavefronts (0-7, two per SIMD): 32 rows each; each loads its rows' activations for the next step from
+//     xh straight into the other half of a double-buffered LDS tile (buffer loads with an LDS destination; rows
+//     past the batch and k past the row read zero through the buffer descriptor), reads A and B fragments from
+//     LDS, 32 MFMAs per step against the current halves.
 // One barrier per step hands the halves over, so decoding (VALU) overlaps the matrix work (MFMA) on the same
 // SIMDs. Epilogue: the 128-point FWHT of each row runs in registers (stages 1, 2, 4, 8 across the 16
 // lanes of a column group, 16, 32, 64 across the accumulator tiles of a lane), then 1/sqrt(128), svh, bias.
@@ -26,7 +26,10 @@ namespace exl3 {
 constexpr int kPfBM = 256;          // rows per workgroup tile
 constexpr int kPfBK = 64;           // k per step
 constexpr int kPfLdB = kPfBK + 8;   // padded LDS row pitch (halves) of the weight tile (n-major)
-constexpr int kPfThreads = 512;
+// MFMA wavefronts (two per SIMD; the decoders are the last four), 16-row tiles of each, and the activation
+// loads per lane and step (256 rows x 8 pieces of 16 bytes over the MFMA wavefronts' lanes)
+constexpr int kPfMfmaWaves = 8, kPfRowTiles = 2, kPfLoadsA = 2048 / (64 * kPfMfmaWaves);
+constexpr int kPfThreads = 64 * kPfMfmaWaves + 256;
 
 template <int K, int CB, int OT>
 __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const uint16_t* __restrict__ xh,
@@ -47,7 +50,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const uint16_t* __r
   const int row0 = blockIdx.y * kPfBM;
   const int KT = k / 16, NT = n / 16;
   const int nsteps = (KT + 3) / 4;
-  const bool decoder = wave >= 4;
+  const bool decoder = wave >= kPfMfmaWaves;
 
   // ---------------- decode role ----------------
   // lane's run in each step: k-tile (t >> 6) of the step, n-tile ((t >> 3) & 7), run g = t & 7
@@ -85,38 +88,39 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const uint16_t* __r
   };
 
   // ---------------- MFMA role ----------------
-  // lane (16q + c): A rows 16 i + c of this wavefront's 64, k 8q .. 8q+7 of each 32-k slice
+  // lane (16q + c): A rows 16 i + c of this wavefront's 32, k 8q .. 8q+7 of each 32-k slice
   const int q = lane >> 4, c = lane & 15;
   const __amdgpu_buffer_rsrc_t rs_x = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(xh), (short)0, (int)((uint32_t)rows * (uint32_t)k * 2u), kBufferFlags);
   // Activations: a step's 256 rows x 64 k (32 KiB) go from xh straight into one of two LDS stages (buffer loads
   // with an LDS destination, no registers), issued by the MFMA wavefronts a step ahead. Lane L of wavefront w's j-th
-  // load fills slot (8 w + j) 64 + L: row (8 w + j) 8 + L / 8 of the tile at position L % 8, which holds the 8 k
+  // load (of kPfLoadsA) fills slot (kPfLoadsA w + j) 64 + L: row (kPfLoadsA w + j) 8 + L / 8 of the tile (so a
+  // wavefront loads the rows it multiplies) at position L % 8, which holds the 8 k
   // at piece (L % 8) ^ (row & 7) (each row is 8 pieces of 16 bytes; with this placement the fragment reads, one
   // piece of 16 consecutive rows, and the 1 KiB load runs are free of LDS bank conflicts). Rows past the batch,
   // pieces past k and steps past the matrix get an offset past the descriptor and read zeros, so a step beyond
   // k contracts zeros with whatever weights the LDS holds.
   const int arow = lane >> 3;
   const int apos8 = ((lane & 7) ^ (arow & 7)) * 8;   // the k offset of this lane's piece (row & 7 = arow & 7)
-  uint32_t abase[8];
+  uint32_t abase[kPfLoadsA];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int r = row0 + (wave * 8 + j) * 8 + arow;
+  for (int j = 0; j < kPfLoadsA; ++j) {
+    const int r = row0 + (wave * kPfLoadsA + j) * 8 + arow;
     abase[j] = r < rows ? ((uint32_t)r * (uint32_t)k + (uint32_t)apos8) * 2u : 0x80000000u;
   }
   // load j of step s into a stage (the builtin's pointer and offset go through plain local variables)
   auto issue_A = [&](int s, u32x4* stage, int j) {
-    u32x4* dst = stage + (wave * 8 + j) * 64;
+    u32x4* dst = stage + (wave * kPfLoadsA + j) * 64;
     uint32_t vo = (s < nsteps && apos8 < k - 64 * s) ? abase[j] + (uint32_t)s * 128u : 0x80000000u;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_x, dst, 16, vo, 0, 0, 0);
   };
-  // fragment of row tile i, 32-k slice sl: row 64 w + 16 i + c, piece 4 sl + q
-  const int afrag = (wave * 64 + c) * 8;
+  // fragment of row tile i, 32-k slice sl: row 32 w + 16 i + c, piece 4 sl + q
+  const int afrag = (wave * (16 * kPfRowTiles) + c) * 8;
   auto read_A = [&](const u32x4* stage, int i, int sl) { return stage[afrag + i * 128 + ((4 * sl + q) ^ (c & 7))]; };
 
-  f32x4 acc[4][8];
+  f32x4 acc[kPfRowTiles][8];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < kPfRowTiles; ++i)
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
@@ -138,7 +142,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const uint16_t* __r
   } else {
     // step 0 into stage 0, landed before the barrier
 #pragma unroll
-    for (int j = 0; j < 8; ++j) issue_A(0, sA0, j);
+    for (int j = 0; j < kPfLoadsA; ++j) issue_A(0, sA0, j);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
   __syncthreads();
@@ -176,24 +180,24 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const uint16_t* __r
   };
   auto mfma_step = [&](int s, const u32x4* a_cur, u32x4* a_next) {
     const int buf = s & 1;
-    u32x4 Af[2][4];
+    u32x4 Af[2][kPfRowTiles];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) Af[0][i] = read_A(a_cur, i, 0);
+    for (int i = 0; i < kPfRowTiles; ++i) Af[0][i] = read_A(a_cur, i, 0);
     u32x4 Bring[kRingB];
 #pragma unroll
     for (int f = 0; f < kRingB - 1; ++f) Bring[f] = read_B(buf, f);
     static_for<0, 16>([&](auto F) {
       constexpr int f = decltype(F)::value;
       constexpr int sl = f >> 3, j = f & 7;
-      if constexpr (f < 8) issue_A(s + 1, a_next, f);   // past the matrix: zeros
+      if constexpr (f < kPfLoadsA) issue_A(s + 1, a_next, f);   // past the matrix: zeros
       if constexpr (f == 4) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) Af[1][i] = read_A(a_cur, i, 1);
+        for (int i = 0; i < kPfRowTiles; ++i) Af[1][i] = read_A(a_cur, i, 1);
       }
       if constexpr (f + kRingB - 1 < 16) Bring[(f + kRingB - 1) % kRingB] = read_B(buf, f + kRingB - 1);
       const f16x8 B = __builtin_bit_cast(f16x8, Bring[f % kRingB]);
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < kPfRowTiles; ++i)
         acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, Af[sl][i]), B, acc[i][j],
                                                            0, 0, 0);
       __builtin_amdgcn_sched_barrier(0);
@@ -221,7 +225,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const uint16_t* __r
     bs[j] = bias ? load_as_f32<OT>(bias, colbase + 16 * j) : 0.f;
   }
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < kPfRowTiles; ++i) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       float v[8];
@@ -243,7 +247,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const uint16_t* __r
           }
         }
       }
-      const int gr = row0 + wave * 64 + 16 * i + 4 * q + r;
+      const int gr = row0 + wave * (16 * kPfRowTiles) + 16 * i + 4 * q + r;
       if (gr < rows) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
