@@ -25,7 +25,6 @@ namespace exl3 {
 
 constexpr int kPfBM = 256;          // rows per workgroup tile
 constexpr int kPfBK = 64;           // k per step
-constexpr int kPfLdB = kPfBK + 8;   // padded LDS row pitch (halves) of the weight tile (n-major)
 // MFMA wavefronts (two per SIMD; the decoders are the last four), 16-row tiles of each, and the activation
 // loads per lane and step (256 rows x 8 pieces of 16 bytes over the MFMA wavefronts' lanes)
 constexpr int kPfMfmaWaves = 8, kPfRowTiles = 2, kPfLoadsA = 2048 / (64 * kPfMfmaWaves);
@@ -37,7 +36,10 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const uint16_t* __r
                                                              const uint16_t* __restrict__ svh,
                                                              const void* __restrict__ bias, void* __restrict__ y) {
   constexpr int TW = 8 * K;
-  __shared__ __attribute__((aligned(16))) uint16_t sB[2][128 * kPfLdB];
+  // the weight tile, two halves of 128 columns x 64 k: column j is a 128-byte row of eight 16-byte pieces
+  // (8 k each), piece p stored at slot p ^ (j & 7), so that the 16 lanes that read one piece of 16 adjacent
+  // columns, and the 8 lanes that store one piece of 8 adjacent columns, spread over the banks
+  __shared__ u32x4 sB[2][128 * 8];
   // the two activation stages as separate arrays: with the stage of each access known at compile time, the
   // compiler sees that the loads into one stage do not touch the fragments read from the other (and waits for
   // none of them before an LDS read)
@@ -77,14 +79,15 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const uint16_t* __r
 #pragma unroll
       for (int i = 0; i < 16; ++i) b[i] = 0u;   // k past the matrix: zero weights
     }
-    uint16_t* blo = sB[buf] + (r_nt * 16 + r_g) * kPfLdB + r_kt * 16;
-    uint16_t* bhi = sB[buf] + (r_nt * 16 + 8 + r_g) * kPfLdB + r_kt * 16;
+    u32x4* blo = sB[buf] + (r_nt * 16 + r_g) * 8;   // column 16 r_nt + g; the hi column is 8 on (same j & 7)
+    u32x4* bhi = blo + 64;
+    const int p0 = (2 * r_kt) ^ r_g, p1 = (2 * r_kt + 1) ^ r_g;   // slots of pieces 2 r_kt, 2 r_kt + 1
     // b[i] holds positions 2i, 2i+1; k pairs of the lo column: (0,1) b0 (2,3) b4 (4,5) b8 (6,7) b12,
     // (8,9) b1 .. (14,15) b13; the hi column: b2 b6 b10 b14, b3 b7 b11 b15
-    reinterpret_cast<u32x4*>(blo)[0] = u32x4{b[0], b[4], b[8], b[12]};
-    reinterpret_cast<u32x4*>(blo)[1] = u32x4{b[1], b[5], b[9], b[13]};
-    reinterpret_cast<u32x4*>(bhi)[0] = u32x4{b[2], b[6], b[10], b[14]};
-    reinterpret_cast<u32x4*>(bhi)[1] = u32x4{b[3], b[7], b[11], b[15]};
+    blo[p0] = u32x4{b[0], b[4], b[8], b[12]};
+    blo[p1] = u32x4{b[1], b[5], b[9], b[13]};
+    bhi[p0] = u32x4{b[2], b[6], b[10], b[14]};
+    bhi[p1] = u32x4{b[3], b[7], b[11], b[15]};
   };
 
   // ---------------- MFMA role ----------------
@@ -173,10 +176,11 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const uint16_t* __r
   // activation fragments half a slice ahead (an LDS read's latency is several MFMAs long); scheduling barriers
   // keep that order, so LDS latency hides behind matrix work instead of stalling it. (Activations fetched two
   // steps ahead through a third stage were level; fetched by each lane into registers, 12% slower.)
-  const uint16_t* bbase = sB[0] + c * kPfLdB + 8 * q;
-  constexpr int kBufHalves = 128 * kPfLdB;
+  // fragment f (slice f >> 3, column tile f & 7): lane (16q + c) reads piece 4 (f >> 3) + q of column
+  // 16 (f & 7) + c
+  const u32x4* bbase = sB[0] + c * 8;
   auto read_B = [&](int buf, int f) {
-    return *reinterpret_cast<const u32x4*>(bbase + buf * kBufHalves + ((f & 7) * 16) * kPfLdB + (f >> 3) * 32);
+    return bbase[buf * 128 * 8 + (f & 7) * 128 + ((4 * (f >> 3) + q) ^ (c & 7))];
   };
   auto mfma_step = [&](int s, const u32x4* a_cur, u32x4* a_next) {
     const int buf = s & 1;
