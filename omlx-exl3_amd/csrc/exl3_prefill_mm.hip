@@ -8,10 +8,11 @@
 // shape so the tiles fill the 256 CUs in whole rounds); wavefront w owns rows 16 TI (w / 2) .. +16 TI and columns
 // 128 (w % 2) .. +128, i.e. 16 TI rows of one 128-column Hadamard block, as TI x 8 accumulator tiles of
 // v_mfma_f32_16x16x32_f16 (32 TI registers; the file is compiled with the accumulators in ordinary VGPRs, where
-// the loop keeps them in place without copies). k advances 64 per step through a double-buffered LDS tile of
-// both operands (k-contiguous rows, XOR-swizzled 16-byte pieces): the next step's global loads go straight into
-// the other LDS half (buffer loads with an LDS destination) while the current step's MFMAs run, one barrier per
-// step.
+// the loop keeps them in place without copies). k advances 64 per step through LDS tiles of both operands
+// (k-contiguous rows, XOR-swizzled 16-byte pieces) that global loads fill directly (buffer loads with an LDS
+// destination) while the MFMAs run, one barrier per step: the activation tile in two stages, loaded a step ahead,
+// the weight tile in three, loaded two steps ahead (its rows, k-contiguous over the whole of k, arrive later than
+// the activations' within a step's MFMAs).
 // Epilogue (per wavefront, in registers): the 128-point FWHT of each row (stages 1, 2, 4, 8 across the 16 lanes
 // of a column group, 16, 32, 64 across the accumulator tiles), 1/sqrt(128) and svh in fp32, a rounding to the
 // output type, then the bias added in the output type (a second rounding). The reference rounds the product to
@@ -32,8 +33,14 @@ constexpr int kMmThreads = 512, kMmWaves = kMmThreads / 64;
 // bank groups (checked exhaustively for both fragment halves), and the loads that fill the tile write 1 KiB
 // contiguous runs, which are conflict-free too.
 __device__ __forceinline__ int mm_pos(int r, int p) { return p ^ (r & 7); }
+// s_waitcnt immediate of gfx9: vmcnt in bits 3:0 and 15:14, expcnt 6:4 (not waited for), lgkmcnt 11:8
+constexpr int waitcnt_vm_lgkm(int vm, int lgkm) {
+  return (vm & 15) | ((vm >> 4) & 3) << 14 | 7 << 4 | (lgkm & 15) << 8;
+}
 __device__ __forceinline__ int mm_slot(int r, int p) { return r * (kMmBK / 8) + mm_pos(r, p); }
-constexpr int kMmSlotsMax = 2 * kMmBN * (kMmBK / 8);   // A and B slots of the largest tile (TI = 4)
+constexpr int kMmSlotsA = kMmBN * (kMmBK / 8);   // 16-byte slots of one A stage at the largest tile (TI = 4)
+constexpr int kMmSlotsB = kMmBN * (kMmBK / 8);   // of one B stage
+constexpr int kMmStagesA = 2, kMmStagesB = 3;
 
 template <int TI>
 struct MmTile {
@@ -72,11 +79,24 @@ __global__ __launch_bounds__(kMmThreads) __attribute__((amdgpu_waves_per_eu(2)))
     const uint16_t* __restrict__ svh, const void* __restrict__ bias, void* __restrict__ y, int ldy, int tiles_m,
     int tiles_n, float* __restrict__ partials, int steps_per_split) {
   using Tl = MmTile<TI>;
-  // [stage][A slots, B slots]: 128 KiB, sized for TI = 4 whatever TI is (one workgroup per CU in every case; an
-  // LDS array whose size depends on a template parameter also makes hipcc drop the kernel's host stub when the
-  // buffer-to-LDS load builtin writes into it)
-  __shared__ u32x4 lds[2][kMmSlotsMax];
-  static_assert(Tl::SA + Tl::SB <= kMmSlotsMax, "LDS tile");
+  // two A stages and three B stages: 160 KiB, sized for TI = 4 whatever TI is (one workgroup per CU in every
+  // case; an LDS array whose size depends on a template parameter also makes hipcc drop the kernel's host stub
+  // when the buffer-to-LDS load builtin writes into it). Each stage is an array of its own, used at compile-time
+  // stage indices: the compiler then sees that a stage being loaded is not one being read, and waits for none of
+  // the loads in flight before an LDS read.
+  __shared__ u32x4 ldsA0[kMmSlotsA], ldsA1[kMmSlotsA];
+  __shared__ u32x4 ldsB0[kMmSlotsB], ldsB1[kMmSlotsB], ldsB2[kMmSlotsB];
+  static_assert(Tl::SA <= kMmSlotsA && Tl::SB <= kMmSlotsB, "LDS tile");
+  static_assert(kMmStagesA == 2 && kMmStagesB == 3, "the stage arrays");
+  auto stage_a = [&](auto I) -> u32x4* {
+    if constexpr (decltype(I)::value % 2 == 0) return ldsA0;
+    else return ldsA1;
+  };
+  auto stage_b = [&](auto I) -> u32x4* {
+    if constexpr (decltype(I)::value % 3 == 0) return ldsB0;
+    else if constexpr (decltype(I)::value % 3 == 1) return ldsB1;
+    else return ldsB2;
+  };
 
   // (wave through readfirstlane: the compiler then knows it is uniform, and the LDS destinations of the tile loads,
   // which go to M0, are computed in scalar registers instead of a VALU readfirstlane before every load)
@@ -114,16 +134,20 @@ __global__ __launch_bounds__(kMmThreads) __attribute__((amdgpu_waves_per_eu(2)))
   // k-split of this workgroup (blockIdx.y): steps s_begin .. s_begin + nsteps - 1 of the k / 64 steps
   const int s_begin = blockIdx.y * steps_per_split;
   const int nsteps = min(k / kMmBK - s_begin, steps_per_split);
-  auto load_stage = [&](int s, int buf) {
+  auto load_a = [&](int s, u32x4* st) {
+    const uint32_t so = (uint32_t)(s_begin + s) * (kMmBK * 2);
+#pragma unroll
+    for (int j = 0; j < Tl::LA; ++j) {
+      u32x4* dst = st + (wave * Tl::LA + j) * 64;
+      uint32_t vo = oa[j];
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_a, dst, 16, vo, so, 0, 0);
+    }
+  };
+  auto load_b = [&](int s, u32x4* st) {
     const uint32_t so = (uint32_t)(s_begin + s) * (kMmBK * 2);
 #pragma unroll
     for (int j = 0; j < Tl::LB; ++j) {
-      if (j < Tl::LA) {
-        u32x4* dst = &lds[buf][(wave * Tl::LA + j) * 64];
-        uint32_t vo = oa[j];
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_a, dst, 16, vo, so, 0, 0);
-      }
-      u32x4* dst = &lds[buf][Tl::SA + (wave * Tl::LB + j) * 64];
+      u32x4* dst = st + (wave * Tl::LB + j) * 64;
       uint32_t vo = ob[j];
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_b, dst, 16, vo, so, 0, 0);
     }
@@ -133,8 +157,7 @@ __global__ __launch_bounds__(kMmThreads) __attribute__((amdgpu_waves_per_eu(2)))
   // i.e. piece 4h + q
   const int q = lane >> 4, c = lane & 15;
   const int wr = (wave >> 1) * (16 * TI), wc = (wave & 1) * 128;
-  auto frag_a = [&](int buf, int r, int h) { return lds[buf][mm_slot(r, 4 * h + q)]; };
-  auto frag_b = [&](int buf, int r, int h) { return lds[buf][Tl::SA + mm_slot(r, 4 * h + q)]; };
+  auto frag = [&](const u32x4* st, int r, int h) { return st[mm_slot(r, 4 * h + q)]; };
 
   f32x4 acc[TI][8];
 #pragma unroll
@@ -144,20 +167,24 @@ __global__ __launch_bounds__(kMmThreads) __attribute__((amdgpu_waves_per_eu(2)))
 
   // Software pipeline over 32-k slices: the fragments of the next slice are read from LDS into one register set
   // while the MFMAs of the current slice use the other, so every LDS read has a slice of MFMAs to land in. A pass
-  // of the loop (step s, LDS half s & 1): wait for step s + 1's tiles and barrier; then the MFMAs of slice 1 of
-  // step s with, after each of the first 8 + TI, one read of slice 0 of step s + 1, and after every third from the
-  // first, one tile load of step s + 2 into half s & 1; then the MFMAs of slice 0 of step s + 1 with the reads of
-  // its slice 1. The order is fixed instruction by instruction (sched_barrier(0) after each group): left to
+  // of the loop (step s; step t's A tile in A stage t % 2, its B tile in B stage t % 3): wait for step s + 1's
+  // tiles and barrier; then the MFMAs of slice 1 of step s with, after each of the first 8 + TI, one read of slice
+  // 0 of step s + 1, and after every third from the first, one tile load: step s + 2's A tile into A stage s % 2,
+  // then step s + 3's B tile into B stage s % 3 (the stages step s used); then the MFMAs of slice 0 of step s + 1
+  // with the reads of its slice 1. Loads complete in issue order, so the wait at the top of a pass leaves the last
+  // pass's B loads (LB per lane) in flight and finds everything older landed: a weight tile has two passes to
+  // arrive, an activation tile one (with one pass for both, down's shape waited ~15% of its time on the weight
+  // loads). The order is fixed instruction by instruction (sched_barrier(0) after each group): left to
   // itself the scheduler issues a pass's tile loads back to back, and the wavefronts, all leaving the barrier
   // together, then wait on the load path instead of feeding the MFMA pipe (at 4,608 rows, one load per three
   // MFMAs measured 6% faster on gate/up than that burst and 2% faster than one per two; on down all three
   // orders were within 1%).
   u32x4 fa0[TI], fb0[8], fa1[TI], fb1[8];
-  auto read_slice = [&](int buf, int h, u32x4 (&fa)[TI], u32x4 (&fb)[8]) {
+  auto read_slice = [&](const u32x4* sa, const u32x4* sb, int h, u32x4 (&fa)[TI], u32x4 (&fb)[8]) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) fb[j] = frag_b(buf, wc + 16 * j + c, h);
+    for (int j = 0; j < 8; ++j) fb[j] = frag(sb, wc + 16 * j + c, h);
 #pragma unroll
-    for (int i = 0; i < TI; ++i) fa[i] = frag_a(buf, wr + 16 * i + c, h);
+    for (int i = 0; i < TI; ++i) fa[i] = frag(sa, wr + 16 * i + c, h);
   };
   auto mma_slice = [&](const u32x4 (&fa)[TI], const u32x4 (&fb)[8]) {
 #pragma unroll
@@ -169,51 +196,86 @@ __global__ __launch_bounds__(kMmThreads) __attribute__((amdgpu_waves_per_eu(2)))
   constexpr int kLoads = Tl::LA + Tl::LB, kEvery = 3;
   static_assert((kLoads - 1) * kEvery < 8 * TI, "every tile load of a pass is issued");
   // MFMA m of a pass's slice, with the LDS read of fragment m (B fragments 0..7, then A fragments) of the slice
-  // read alongside into (fa, fb), and tile load m / kEvery of step sl when m is a multiple of kEvery
-  auto pass_slice = [&](auto with_loads, int buf, int h, int sl, const u32x4 (&fa_use)[TI],
-                        const u32x4 (&fb_use)[8], u32x4 (&fa)[TI], u32x4 (&fb)[8]) {
-    const uint32_t so = (uint32_t)(s_begin + sl) * (kMmBK * 2);
+  // from stages (ra, rb) alongside into (fa, fb), and tile load m / kEvery when m is a multiple of kEvery: A loads
+  // of step la into stage wa first, then B loads of step lb into stage wb
+  auto pass_slice = [&](auto with_loads, const u32x4* ra, const u32x4* rb, int h, u32x4* wa, int la, u32x4* wb,
+                        int lb, const u32x4 (&fa_use)[TI], const u32x4 (&fb_use)[8], u32x4 (&fa)[TI],
+                        u32x4 (&fb)[8]) {
+    const uint32_t soa = (uint32_t)(s_begin + la) * (kMmBK * 2), sob = (uint32_t)(s_begin + lb) * (kMmBK * 2);
     static_for<0, 8 * TI>([&](auto M) {
       constexpr int m = decltype(M)::value;
       acc[m / 8][m % 8] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_f16x8(fa_use[m / 8]), as_f16x8(fb_use[m % 8]),
                                                                   acc[m / 8][m % 8], 0, 0, 0);
-      if constexpr (m < 8) fb[m] = frag_b(buf ^ 1, wc + 16 * m + c, h);
-      else if constexpr (m < 8 + TI) fa[m - 8] = frag_a(buf ^ 1, wr + 16 * (m - 8) + c, h);
+      if constexpr (m < 8) fb[m] = frag(rb, wc + 16 * m + c, h);
+      else if constexpr (m < 8 + TI) fa[m - 8] = frag(ra, wr + 16 * (m - 8) + c, h);
       if constexpr (decltype(with_loads)::value && m % kEvery == 0 && m / kEvery < kLoads) {
         constexpr int j = m / kEvery;
         if constexpr (j < Tl::LA) {
-          u32x4* dst = &lds[buf][(wave * Tl::LA + j) * 64];
+          u32x4* dst = wa + (wave * Tl::LA + j) * 64;
           uint32_t vo = oa[j];
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_a, dst, 16, vo, so, 0, 0);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_a, dst, 16, vo, soa, 0, 0);
         } else {
-          u32x4* dst = &lds[buf][Tl::SA + (wave * Tl::LB + (j - Tl::LA)) * 64];
+          u32x4* dst = wb + (wave * Tl::LB + (j - Tl::LA)) * 64;
           uint32_t vo = ob[j - Tl::LA];
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_b, dst, 16, vo, so, 0, 0);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_b, dst, 16, vo, sob, 0, 0);
         }
       }
       __builtin_amdgcn_sched_barrier(0);
     });
   };
-
-  load_stage(0, 0);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  // step 1's tiles (step 0's again when there is no step 1: a harmless reload of the idle half)
-  load_stage(nsteps > 1 ? 1 : 0, 1);
-  read_slice(0, 0, fa0, fb0);
-  read_slice(0, 1, fa1, fb1);
-  mma_slice(fa0, fb0);
-  for (int s = 0; s + 1 < nsteps; ++s) {
-    const int buf = s & 1;
+  // Pass s for s % 6 = U (stage indices known at compile time). Steps past the split are replaced by step
+  // nsteps - 1: a harmless reload into a stage that no later pass reads.
+  const int last = nsteps - 1;
+  static_assert(Tl::LB == 4, "the pass's wait count");
+  auto pass = [&](auto U, int s) {
+    constexpr int u = decltype(U)::value;
     __builtin_amdgcn_sched_barrier(0);
-    // step s + 1's tiles have landed in LDS (vmcnt) and every wavefront's reads of step s are done (the barrier
-    // waits for LDS reads) before any wavefront goes on
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    // step s + 2's tiles into the half step s used (the last pass reloads step s + 1 there, unused: the loop has
-    // no branch, which would split its body and make the compiler copy the accumulators at the join)
-    pass_slice(std::true_type{}, buf, 0, s + 2 < nsteps ? s + 2 : s + 1, fa1, fb1, fa0, fb0);
-    pass_slice(std::false_type{}, buf, 1, 0, fa0, fb0, fa1, fb1);
+    // step s + 1's tiles have landed in LDS (everything but the newest LB loads, step s + 2's B tile, is done),
+    // and every wavefront's LDS reads of step s are done, before any wavefront goes on and overwrites that step's
+    // stages (the barrier without __syncthreads' release fence, which would also wait for the B loads still in
+    // flight; the acquire fence keeps every later LDS read below the barrier)
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm(Tl::LB, 0));
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    __builtin_amdgcn_sched_barrier(0);
+    const std::integral_constant<int, u + 1> next{};
+    pass_slice(std::true_type{}, stage_a(next), stage_b(next), 0, stage_a(U), min(s + 2, last), stage_b(U),
+               min(s + 3, last), fa1, fb1, fa0, fb0);
+    pass_slice(std::false_type{}, stage_a(next), stage_b(next), 1, nullptr, 0, nullptr, 0, fa0, fb0, fa1, fb1);
+  };
+
+  // Steps 0, 1 and step 2's B tile, in the order the loop's last two passes leave their loads at the loop's head
+  // (an A tile, then a B tile, per pass: the compiler's wait accounting is then the same on both paths into the
+  // loop); step 0's tiles landed, the rest in flight.
+  load_b(0, ldsB0);
+  load_a(0, ldsA0);
+  load_b(min(1, last), ldsB1);
+  load_a(min(1, last), ldsA1);
+  load_b(min(2, last), ldsB2);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm(2 * Tl::LB + Tl::LA, 15));
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  __builtin_amdgcn_sched_barrier(0);
+  read_slice(ldsA0, ldsB0, 0, fa0, fb0);
+  read_slice(ldsA0, ldsB0, 1, fa1, fb1);
+  mma_slice(fa0, fb0);
+  // passes s = 0 .. nsteps - 2, six per iteration (the A stages repeat every 2 steps, the B stages every 3); the
+  // loop is left after whichever pass is the last
+  for (int s = 0;;) {
+    if (s + 1 >= nsteps) break;
+    pass(std::integral_constant<int, 0>{}, s++);
+    if (s + 1 >= nsteps) break;
+    pass(std::integral_constant<int, 1>{}, s++);
+    if (s + 1 >= nsteps) break;
+    pass(std::integral_constant<int, 2>{}, s++);
+    if (s + 1 >= nsteps) break;
+    pass(std::integral_constant<int, 3>{}, s++);
+    if (s + 1 >= nsteps) break;
+    pass(std::integral_constant<int, 4>{}, s++);
+    if (s + 1 >= nsteps) break;
+    pass(std::integral_constant<int, 5>{}, s++);
   }
   mma_slice(fa1, fb1);
   // no LDS-bound load is left in flight when the workgroup ends
@@ -252,7 +314,7 @@ __global__ __launch_bounds__(kMmThreads) __attribute__((amdgpu_waves_per_eu(2)))
     sv[j] = f16_to_f32(svh[colbase + 16 * j]);
     bs[j] = has_bias ? load_as_f32<OT>(bias, colbase + 16 * j) : 0.f;
   }
-  uint16_t* stage = reinterpret_cast<uint16_t*>(&lds[0][0]) + wave * (16 * 128);
+  uint16_t* stage = reinterpret_cast<uint16_t*>(ldsA0) + wave * (16 * 128);
   auto stage_at = [](int R, int col) { return R * 128 + ((((col >> 3) ^ (2 * ((R >> 2) & 3)))) << 3) + (col & 7); };
   // compile-time row indices (static_for) keep acc in registers whatever the unroller decides
   static_for<0, TI>([&](auto I) {
