@@ -416,7 +416,7 @@ __device__ __forceinline__ void store8(void* base, size_t i0, const float (&v)[8
 // ------------------------------------------------------------------------------------------------
 // v from lane (lane ^ H) of the same 16-lane row, H = 1, 2, 4, 8, by DPP moves:
 // quad_perm [1,0,3,2] and [2,3,0,1] for 1 and 2; row_half_mirror (lane ^ 7) then quad_perm [3,2,1,0] (^ 3) for 4;
-// row_mirror (lane ^ 15) then row_half_mirror (^ 7) for 8. Every lane reads a lane of its own row, so a row that
+// row_ror:8 (a rotation by half a row is lane ^ 8) for 8. Every lane reads a lane of its own row, so a row that
 // is active as a whole never reads an inactive lane (bound_ctrl never applies).
 template <int H>
 __device__ __forceinline__ float lane_xor(float v) {
@@ -427,7 +427,7 @@ __device__ __forceinline__ float lane_xor(float v) {
   if constexpr (H == 1) r = dpp(x, std::integral_constant<int, 0xB1>{});
   else if constexpr (H == 2) r = dpp(x, std::integral_constant<int, 0x4E>{});
   else if constexpr (H == 4) r = dpp(dpp(x, std::integral_constant<int, 0x141>{}), std::integral_constant<int, 0x1B>{});
-  else r = dpp(dpp(x, std::integral_constant<int, 0x140>{}), std::integral_constant<int, 0x141>{});
+  else r = dpp(x, std::integral_constant<int, 0x128>{});
   return __builtin_bit_cast(float, r);
 }
 
