@@ -324,11 +324,12 @@ enum DType : int { kF16 = 0, kBF16 = 1, kF32 = 2 };
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __builtin_bit_cast(float, (uint32_t)b << 16); }
 
-__device__ __forceinline__ uint16_t f32_to_bf16(float v) {   // round to nearest even, NaN kept quiet
-  uint32_t u = __builtin_bit_cast(uint32_t, v);
-  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40u);
-  u += 0x7FFFu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
+// fp32 -> bf16 with round-to-nearest-even (gfx950's v_cvt_pk_bf16_f32; fp32 denormals are kept in these kernels'
+// float mode, so they round as normal values do; a NaN stays a NaN). The empty asm pins the fp32 value, as in
+// f32_to_f16 below.
+__device__ __forceinline__ uint16_t f32_to_bf16(float v) {
+  asm volatile("" : "+v"(v));
+  return __builtin_bit_cast(uint16_t, (__bf16)v);
 }
 
 __device__ __forceinline__ float f16_to_f32(uint16_t b) { return (float)__builtin_bit_cast(_Float16, b); }
