@@ -10,10 +10,10 @@
 //   decode wavefronts (8-11, one per SIMD): one trellis run per lane per step (4 k-tiles x 8 n-tiles x 8 runs = 256 runs),
 //     prefetched two steps ahead, decoded into the next step's half of a double-buffered LDS weight tile
 //     (n-major, 16-byte pair groups, the B-operand layout of v_mfma_f32_16x16x32_f16);
-//   MFMA wavefronts (0-7, two per SIMD): 32 rows each; each loads its rows' activations for the next step from
-//     xh straight into the other half of a double-buffered LDS tile (buffer loads with an LDS destination; rows
-//     past the batch and k past the row read zero through the buffer descriptor), reads A and B fragments from
-//     LDS, 32 MFMAs per step against the current halves.
+//   MFMA wavefronts (0-7, two per SIMD): 32 rows each; each loads its rows' activations two steps ahead from
+//     xh straight into one of three LDS stages (buffer loads with an LDS destination; rows past the batch and k
+//     past the row read zero through the buffer descriptor), reads A and B fragments from LDS, 32 MFMAs per
+//     step against the current stage and weight half.
 // One barrier per step hands the halves over, so decoding (VALU) overlaps the matrix work (MFMA) on the same
 // SIMDs. Epilogue: the 128-point FWHT of each row runs in registers (stages 1, 2, 4, 8 across the 16
 // lanes of a column group, 16, 32, 64 across the accumulator tiles of a lane), then 1/sqrt(128), svh, bias.
@@ -29,6 +29,10 @@ constexpr int kPfBK = 64;           // k per step
 // loads per lane and step (256 rows x 8 pieces of 16 bytes over the MFMA wavefronts' lanes)
 constexpr int kPfMfmaWaves = 8, kPfRowTiles = 2, kPfLoadsA = 2048 / (64 * kPfMfmaWaves);
 constexpr int kPfThreads = 64 * kPfMfmaWaves + 256;
+// s_waitcnt immediate of gfx9: vmcnt in bits 3:0 and 15:14, expcnt 6:4 (not waited for), lgkmcnt 11:8
+constexpr int pf_waitcnt_vm(int vm, int lgkm = 15) {
+  return (vm & 15) | ((vm >> 4) & 3) << 14 | 7 << 4 | (lgkm & 15) << 8;
+}
 
 template <int K, int CB, int OT>
 __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const uint16_t* __restrict__ xh,
@@ -40,10 +44,10 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const uint16_t* __r
   // (8 k each), piece p stored at slot p ^ (j & 7), so that the 16 lanes that read one piece of 16 adjacent
   // columns, and the 8 lanes that store one piece of 8 adjacent columns, spread over the banks
   __shared__ u32x4 sB[2][128 * 8];
-  // the two activation stages as separate arrays: with the stage of each access known at compile time, the
-  // compiler sees that the loads into one stage do not touch the fragments read from the other (and waits for
+  // the three activation stages as separate arrays: with the stage of each access known at compile time, the
+  // compiler sees that the loads into one stage do not touch the fragments read from another (and waits for
   // none of them before an LDS read)
-  __shared__ u32x4 sA0[kPfBM * 8], sA1[kPfBM * 8];
+  __shared__ u32x4 sA0[kPfBM * 8], sA1[kPfBM * 8], sA2[kPfBM * 8];
 
   // (wave through readfirstlane: uniform, so the LDS destinations of the activation loads, which go to M0, are
   // computed in scalar registers)
@@ -95,8 +99,8 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const uint16_t* __r
   const int q = lane >> 4, c = lane & 15;
   const __amdgpu_buffer_rsrc_t rs_x = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(xh), (short)0, (int)((uint32_t)rows * (uint32_t)k * 2u), kBufferFlags);
-  // Activations: a step's 256 rows x 64 k (32 KiB) go from xh straight into one of two LDS stages (buffer loads
-  // with an LDS destination, no registers), issued by the MFMA wavefronts a step ahead. Lane L of wavefront w's j-th
+  // Activations: a step's 256 rows x 64 k (32 KiB) go from xh straight into one of three LDS stages (buffer loads
+  // with an LDS destination, no registers), issued by the MFMA wavefronts two steps ahead. Lane L of wavefront w's j-th
   // load (of kPfLoadsA) fills slot (kPfLoadsA w + j) 64 + L: row (kPfLoadsA w + j) 8 + L / 8 of the tile (so a
   // wavefront loads the rows it multiplies) at position L % 8, which holds the 8 k
   // at piece (L % 8) ^ (row & 7) (each row is 8 pieces of 16 bytes; with this placement the fragment reads, one
@@ -142,13 +146,20 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const uint16_t* __r
     // one k-step (k <= 64): the padded steps also read the second half, which no step writes; fill it with
     // zero weights (step 1 lies past the matrix) so that LDS left over from earlier kernels is never read
     if (nsteps == 1) store_run(1, 1, w, wp);
+    __syncthreads();
   } else {
-    // step 0 into stage 0, landed before the barrier
+    // steps 0 and 1 into stages 0 and 1, step 0 landed before the barrier (loads complete in issue order: the
+    // wait leaves step 1's kPfLoadsA in flight; a bare barrier, since __syncthreads would wait for them too)
 #pragma unroll
     for (int j = 0; j < kPfLoadsA; ++j) issue_A(0, sA0, j);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int j = 0; j < kPfLoadsA; ++j) issue_A(1, sA1, j);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(pf_waitcnt_vm(kPfLoadsA));
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    __builtin_amdgcn_sched_barrier(0);
   }
-  __syncthreads();
 
   // The two roles run separate loops with one barrier per step each (same count), so the compiler's wait
   // analysis of one role never sees the other role's loads. The step count is padded to a multiple of two
@@ -169,20 +180,20 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const uint16_t* __r
     }
     return;
   }
-  // MFMA role: step s reads its activations from stage s % 2 and issues step s + 1's into the other stage (read
-  // last in step s - 1), one load per group of four MFMAs over the first half of the step; they have landed
-  // before the step's closing barrier. Within a step, the 16 weight fragments (2 slices x 8 column tiles) are
+  // MFMA role: step s reads its activations from stage s % 3 and issues step s + 2's into stage (s + 2) % 3 (read
+  // last in step s - 1), one load per group of four MFMAs over the first half of the step; the step's closing wait
+  // leaves those in flight (loads complete in issue order) and finds step s + 1's landed. Within a step, the 16 weight fragments (2 slices x 8 column tiles) are
   // read through a ring of five, four fragments ahead of the MFMAs that use them, and the second slice's
   // activation fragments half a slice ahead (an LDS read's latency is several MFMAs long); scheduling barriers
-  // keep that order, so LDS latency hides behind matrix work instead of stalling it. (Activations fetched two
-  // steps ahead through a third stage were level; fetched by each lane into registers, 12% slower.)
+  // keep that order, so LDS latency hides behind matrix work instead of stalling it. (Activations fetched a step
+  // ahead through two stages: 2% slower on gate/up; fetched by each lane into registers, 12% slower.)
   // fragment f (slice f >> 3, column tile f & 7): lane (16q + c) reads piece 4 (f >> 3) + q of column
   // 16 (f & 7) + c
   const u32x4* bbase = sB[0] + c * 8;
   auto read_B = [&](int buf, int f) {
     return bbase[buf * 128 * 8 + (f & 7) * 128 + ((4 * (f >> 3) + q) ^ (c & 7))];
   };
-  auto mfma_step = [&](int s, const u32x4* a_cur, u32x4* a_next) {
+  auto mfma_step = [&](int s, const u32x4* a_cur, u32x4* a_next2) {
     const int buf = s & 1;
     u32x4 Af[2][kPfRowTiles];
 #pragma unroll
@@ -193,7 +204,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const uint16_t* __r
     static_for<0, 16>([&](auto F) {
       constexpr int f = decltype(F)::value;
       constexpr int sl = f >> 3, j = f & 7;
-      if constexpr (f < kPfLoadsA) issue_A(s + 1, a_next, f);   // past the matrix: zeros
+      if constexpr (f < kPfLoadsA) issue_A(s + 2, a_next2, f);   // past the matrix: zeros
       if constexpr (f == 4) {
 #pragma unroll
         for (int i = 0; i < kPfRowTiles; ++i) Af[1][i] = read_A(a_cur, i, 1);
@@ -206,15 +217,24 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const uint16_t* __r
                                                            0, 0, 0);
       __builtin_amdgcn_sched_barrier(0);
     });
-    // step s + 1's activations have landed in LDS before any wavefront goes on
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
+    // step s + 1's activations have landed in LDS (all but the newest kPfLoadsA loads, step s + 2's) and this
+    // wavefront's LDS reads of step s are done before any wavefront goes on and overwrites that stage
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(pf_waitcnt_vm(kPfLoadsA, 0));
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    __builtin_amdgcn_sched_barrier(0);
   };
-  // two steps per trip (nsteps_pad is even), so that each step's stages are known at compile time
-  for (int s0 = 0; s0 < nsteps_pad; s0 += kStepsPerGroup) {
-    mfma_step(s0, sA0, sA1);
-    mfma_step(s0 + 1, sA1, sA0);
+  // three steps per trip (the activation stages repeat every 3 steps), so that each step's stages are known at
+  // compile time, then the last nsteps_pad % 3 steps (nsteps_pad is the decode role's count)
+  int s = 0;
+  for (; s + 3 <= nsteps_pad; s += 3) {
+    mfma_step(s, sA0, sA2);
+    mfma_step(s + 1, sA1, sA0);
+    mfma_step(s + 2, sA2, sA1);
   }
+  if (s < nsteps_pad) mfma_step(s, sA0, sA2);
+  if (s + 1 < nsteps_pad) mfma_step(s + 1, sA1, sA0);
   // no LDS-bound load is left in flight when the workgroup ends
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
