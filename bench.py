@@ -162,6 +162,9 @@ def cpu_baseline(seconds_budget: float = 30.0) -> dict:
 
 
 MFMA_F16_PEAK_TFLOPS = 2500.0
+# each prefill form runs untimed for at least this long first: two passes leave the clocks short of their
+# sustained MFMA state, and the first form timed read ~8% slow behind them
+PREFILL_WARM_S = 0.6
 # weight bytes read per decode token of the 64-layer 27B-shape decoder at K = 6 (layers' trellis + head)
 DECODE_BYTES_PER_TOKEN = 64 * 255_590_400 + 583_434_240
 # 27B projections as separate tensors (their K drawn per tensor in the mixed-bitrate configuration)
@@ -316,11 +319,11 @@ def prefill_benchmark(pk, torch, dev, rows=4608, reps=6) -> dict:
     at K = 6. Forms timed: "matmul" (W_inner^T reconstructed, then the hand-written MFMA GEMM with the output
     rotation in its epilogue: prefill_gemm's default), "fused" (trellis tiles reconstructed in LDS, MFMA, Hadamard
     epilogue, one launch), and for comparison "blas" (reconstruct, hipBLASLt fp16 GEMM with the tabled solution,
-    output rotation: the reference's structure on the platform BLAS). Every form first runs twice over the three
-    projections (warm clocks, allocator, plans); a form's figure is then the GPU time of `reps` back-to-back
-    passes over gate, up and down (HIP events, the region starting behind one more untimed pass so the GPU is
-    busy when it opens); per projection the same with that projection alone. TFLOP/s = 2 M k n / time,
-    against the 2.5 PFLOP/s dense fp16 MFMA peak."""
+    output rotation: the reference's structure on the platform BLAS). Every form first runs over the three
+    projections untimed, at least twice and for at least PREFILL_WARM_S seconds (warm clocks, allocator, plans);
+    a form's figure is then the GPU time of `reps` back-to-back passes over gate, up and down (HIP events, the
+    region starting behind one more untimed pass so the GPU is busy when it opens); per projection the same with
+    that projection alone. TFLOP/s = 2 M k n / time, against the 2.5 PFLOP/s dense fp16 MFMA peak."""
     g = torch.Generator(device=dev).manual_seed(5)
     table_ok = False
     if os.path.exists(GEMM_TABLE):
@@ -361,10 +364,13 @@ def prefill_benchmark(pk, torch, dev, rows=4608, reps=6) -> dict:
     names = [sh[0] for sh in shapes]
     per, tot = {}, {}
     for path in paths:
-        for _ in range(2):
+        warm_until = time.perf_counter() + PREFILL_WARM_S
+        passes = 0
+        while passes < 2 or time.perf_counter() < warm_until:
             for nm in names:
                 call(nm, path)
-        torch.cuda.synchronize()
+            torch.cuda.synchronize()
+            passes += 1
         ms_all = timed(names, path)
         tot[path] = (sum(flop.values()), ms_all)
         per[path] = {}
