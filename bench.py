@@ -165,6 +165,8 @@ MFMA_F16_PEAK_TFLOPS = 2500.0
 # each prefill form runs untimed for at least this long first: two passes leave the clocks short of their
 # sustained MFMA state, and the first form timed read ~8% slow behind them
 PREFILL_WARM_S = 0.6
+# the decode GEMV's untimed eager passes run at least this long before its first timing
+GEMV_WARM_S = 0.6
 # weight bytes read per decode token of the 64-layer 27B-shape decoder at K = 6 (layers' trellis + head)
 DECODE_BYTES_PER_TOKEN = 64 * 255_590_400 + 583_434_240
 # 27B projections as separate tensors (their K drawn per tensor in the mixed-bitrate configuration)
@@ -526,10 +528,15 @@ def main() -> int:
         for _name, plan, xh, trs, out, _b in items:
             plan(xh, trs, out=out)
 
-    # eager pass (plans, kernels)
-    for items in layers:
-        run_layer(items)
-    torch.cuda.synchronize()
+    # eager passes (plans, kernels), at least one and for at least GEMV_WARM_S seconds: the clocks settle under
+    # load before the first timing
+    warm_until = time.perf_counter() + GEMV_WARM_S
+    passes = 0
+    while passes < 1 or time.perf_counter() < warm_until:
+        for items in layers:
+            run_layer(items)
+        torch.cuda.synchronize()
+        passes += 1
 
     # ---- per-shape launch durations: one shape's launches of all layers (different weights each) captured in
     # one graph and replayed; HIP events on the replay stream around the timed replays, divided by the launches
