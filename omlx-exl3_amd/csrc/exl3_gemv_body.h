@@ -262,17 +262,23 @@ __device__ __forceinline__ void gemv_body(const GemvArgs a, u32x4* xs, float (*b
   const uint32_t kstride = (uint32_t)NT * TW;   // words per k-tile row of the member's trellis
   // trellis of this split: k-tile rows [kt0, kt1); lane q of iteration it reads row kt0 + 4 it + q. The
   // descriptor ends at the split's end: prefetches past it (and k-tiles past it) read zeros, no traffic.
-  const __amdgpu_buffer_rsrc_t rs_t = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint32_t*>(tr + (size_t)kt0 * kstride), (short)0, (int)((uint32_t)nkt * kstride * 4u), kBufferFlags);
+  const uint32_t split_bytes = (uint32_t)nkt * kstride * 4u;
+  char* const tr_split = reinterpret_cast<char*>(const_cast<uint32_t*>(tr + (size_t)kt0 * kstride));
   // local iteration j of this k-group is the split's iteration kg + WK j
   const uint32_t vo_t = ((uint32_t)(q + 4 * kg) * kstride + (uint32_t)nt_local * TW + K * g) * 4u;
   const uint32_t vo_wp = ((uint32_t)(q + 4 * kg) * kstride + (uint32_t)nt_local * TW + (K * g + TW - 1) % TW) * 4u;
   const uint32_t step_t = 16u * kstride * (uint32_t)WK;   // bytes per local iteration (4 WK k-tile rows)
 
   auto issue_it = [&](Stage<K>& st, int it) {
-    // the advance goes into the per-lane offset, which the descriptor's range check covers
+    // the advance moves the descriptor's base and shortens its range by as much (wavefront-uniform, scalar
+    // instructions), so the range check covers it as before while the lane offsets stay fixed: no per-lane
+    // address additions. From the split's end on, the range is empty and the loads return zeros.
+    // (signed arithmetic: both stay below 2^31, and max(., 0) has a scalar form where a saturating subtraction
+    // would be a vector instruction and move the descriptor into vector registers)
     const uint32_t adv = (uint32_t)it * step_t;
-    load_run<K>(rs_t, vo_t + adv, vo_wp + adv, 0u, st.w, st.wp);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        tr_split + adv, (short)0, max((int)split_bytes - (int)adv, 0), kBufferFlags);
+    load_run<K>(rs, vo_t, vo_wp, 0u, st.w, st.wp);
   };
 
   // ---- this split's activations for LDS: loads issued before the trellis prefetch ----
